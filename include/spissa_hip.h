@@ -1,0 +1,222 @@
+/*
+ * spissa_hip.h -- C ABI of the MI355X (gfx950) attention path for the Spissa
+ * runtime: RoPE, the per-layer KV cache, cached SDPA (decode and causal GQA
+ * prefill), and the Gemma 3 QK-norm.
+ *
+ * Every symbol here replaces one Rust item of crates/spissa-runtime; the
+ * citation next to each declaration names it (paths relative to the
+ * reference repository root). The ABI is plain C: pointers, sizes and status
+ * codes, no C++ or torch types.
+ *
+ * Two kinds of entry points:
+ *   - drop-in (no suffix): host pointers, exactly the Rust argument meaning and
+ *     error behaviour; synchronous; results are host-visible on return;
+ *   - device (`_device` suffix): device pointers, asynchronous on the
+ *     session's HIP stream; device-side errors (invalid softmax denominator)
+ *     are reported by the next spissa_session_sync().
+ *
+ * Status codes map onto RuntimeError variants
+ * (crates/spissa-runtime/src/error.rs:6-54). Validation always happens before
+ * any mutation, as in the reference. No call aborts or lets an exception out.
+ */
+#ifndef SPISSA_HIP_H
+#define SPISSA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    SPISSA_OK = 0,
+    SPISSA_ERR_SHAPE = 1,               /* RuntimeError::Shape (error.rs:12) */
+    SPISSA_ERR_INVALID_TENSOR_DATA = 2, /* RuntimeError::InvalidTensorData (error.rs:24) */
+    SPISSA_ERR_DEVICE = 3,              /* HIP runtime failure; no reference counterpart */
+    SPISSA_ERR_ARGUMENT = 4             /* null handle or pointer; no reference counterpart */
+} spissa_status;
+
+/* Thread-local message of the last failing call on this thread. */
+const char *spissa_last_error(void);
+const char *spissa_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* Sessions: one device, one HIP stream, one growable device workspace.     */
+/* The reference has no counterpart (it is synchronous, single-threaded:     */
+/* crates/spissa-runtime/src/rotary.rs:335-415); a session is the device     */
+/* context the drop-in calls run in. Drop-in calls use the calling thread's  */
+/* default session (current HIP device at first use).                       */
+/* ------------------------------------------------------------------------ */
+typedef struct spissa_session spissa_session;
+
+/* stream: an existing hipStream_t to run on (not owned), or NULL to create one. */
+int spissa_session_create(int device, void *stream, spissa_session **out);
+void spissa_session_destroy(spissa_session *s);
+int spissa_default_session(spissa_session **out);
+/* Wait for all work of the session; returns INVALID_TENSOR_DATA if a device
+ * kernel saw an invalid softmax denominator since the last sync. */
+int spissa_session_sync(spissa_session *s);
+void *spissa_session_stream(spissa_session *s);
+int spissa_session_device(const spissa_session *s);
+
+/* ------------------------------------------------------------------------ */
+/* KV cache: rotary.rs:195-318 (KvCache). Device-resident, appended in place. */
+/* Layout of keys and values in HBM: [max_seq_len, num_heads, head_dim] f32,  */
+/* row-major, so the first len rows are byte-identical to KvCache::keys().    */
+/* ------------------------------------------------------------------------ */
+typedef struct spissa_kv_cache spissa_kv_cache;
+
+/* rotary.rs:206-224 KvCache::new (on the calling thread's default session). */
+int spissa_kv_cache_new(size_t num_heads, size_t head_dim, size_t max_seq_len,
+                        spissa_kv_cache **out);
+/* Same, bound to an explicit session. */
+int spissa_kv_cache_new_in(spissa_session *s, size_t num_heads, size_t head_dim,
+                           size_t max_seq_len, spissa_kv_cache **out);
+/* Drop impl of KvCache. */
+void spissa_kv_cache_free(spissa_kv_cache *c);
+/* #[derive(Clone)] on KvCache (rotary.rs:195). */
+int spissa_kv_cache_clone(const spissa_kv_cache *c, spissa_kv_cache **out);
+/* rotary.rs:226-256 KvCache::append (host buffers; validates before mutating). */
+int spissa_kv_cache_append(spissa_kv_cache *c, const float *keys, size_t keys_len,
+                           const float *values, size_t values_len, size_t token_count);
+/* Same contract with device buffers of token_count*num_heads*head_dim floats. */
+int spissa_kv_cache_append_device(spissa_kv_cache *c, const float *d_keys,
+                                  const float *d_values, size_t token_count);
+/* rotary.rs:258-262 KvCache::clear */
+void spissa_kv_cache_clear(spissa_kv_cache *c);
+/* rotary.rs:264-278 KvCache::truncate */
+int spissa_kv_cache_truncate(spissa_kv_cache *c, size_t len);
+/* rotary.rs:280-305 accessors */
+size_t spissa_kv_cache_len(const spissa_kv_cache *c);
+int spissa_kv_cache_is_empty(const spissa_kv_cache *c);
+size_t spissa_kv_cache_max_seq_len(const spissa_kv_cache *c);
+size_t spissa_kv_cache_num_heads(const spissa_kv_cache *c);
+size_t spissa_kv_cache_head_dim(const spissa_kv_cache *c);
+size_t spissa_kv_cache_resident_bytes(const spissa_kv_cache *c);
+/* rotary.rs:307-313 keys()/values(): copy len*num_heads*head_dim floats to host. */
+int spissa_kv_cache_read_keys(const spissa_kv_cache *c, float *dst, size_t dst_len);
+int spissa_kv_cache_read_values(const spissa_kv_cache *c, float *dst, size_t dst_len);
+/* Device base pointers of the resident buffers (fast path, no reference counterpart). */
+const float *spissa_kv_cache_device_keys(const spissa_kv_cache *c);
+const float *spissa_kv_cache_device_values(const spissa_kv_cache *c);
+
+/* ------------------------------------------------------------------------ */
+/* RoPE: rotary.rs:6-193                                                    */
+/* ------------------------------------------------------------------------ */
+
+/* rotary.rs:6-14 RotaryEmbeddingConfig */
+typedef struct {
+    size_t seq_len;
+    size_t num_heads;
+    size_t head_dim;
+    size_t rotary_dim;
+    float base;
+    size_t position_offset;
+} spissa_rotary_config;
+
+/* rotary.rs:17-38 gpt_neox_rotary_dim */
+int spissa_gpt_neox_rotary_dim(size_t head_dim, float rotary_pct, size_t *out);
+/* rotary.rs:45-69 apply_gpt_neox_rotary_inplace */
+int spissa_apply_gpt_neox_rotary_inplace(float *q, size_t q_len, float *k, size_t k_len,
+                                         const spissa_rotary_config *cfg);
+/* rotary.rs:75-125 apply_llama_rotary_inplace; freq_scale may be NULL (Option::None). */
+int spissa_apply_llama_rotary_inplace(float *q, size_t q_len, float *k, size_t k_len,
+                                      size_t q_heads, size_t k_heads,
+                                      const spissa_rotary_config *cfg, const float *freq_scale,
+                                      size_t freq_scale_len);
+/* rotary.rs:137-186 apply_gemma_rotary_inplace */
+int spissa_apply_gemma_rotary_inplace(float *q, size_t q_len, float *k, size_t k_len,
+                                      size_t q_heads, size_t k_heads,
+                                      const spissa_rotary_config *cfg, float position_divisor);
+
+/* Resident cos/sin table for positions [0, max_positions): computed once on
+ * the host with the exact per-(position, pair) formulas of rotary.rs:454-465
+ * (LLAMA, NEOX) or rotary.rs:168,188-193 (GEMMA) and applied on the device,
+ * so device RoPE is bit-identical to the drop-in call. */
+typedef enum { SPISSA_ROPE_LLAMA = 0, SPISSA_ROPE_GEMMA = 1, SPISSA_ROPE_NEOX = 2 } spissa_rope_kind;
+typedef struct spissa_rope_table spissa_rope_table;
+int spissa_rope_table_new(spissa_session *s, int kind, size_t rotary_dim, float base,
+                          float position_divisor, const float *freq_scale, size_t freq_scale_len,
+                          size_t max_positions, spissa_rope_table **out);
+void spissa_rope_table_free(spissa_rope_table *t);
+/* Device RoPE on q [seq_len, q_heads, head_dim] and k [seq_len, k_heads, head_dim]
+ * at absolute positions position_offset + s. */
+int spissa_rope_apply_device(spissa_session *s, const spissa_rope_table *t, float *d_q,
+                             float *d_k, size_t seq_len, size_t q_heads, size_t k_heads,
+                             size_t head_dim, size_t position_offset);
+
+/* ------------------------------------------------------------------------ */
+/* RMSNorm / Gemma QK-norm                                                  */
+/* ------------------------------------------------------------------------ */
+
+/* ops.rs:159-179 rms_norm (bit-identical: sequential sum of squares per row). */
+int spissa_rms_norm(const float *x, size_t x_len, const float *weight, size_t weight_len,
+                    size_t rows, size_t cols, float eps, float *out, size_t out_len);
+int spissa_rms_norm_device(spissa_session *s, const float *d_x, const float *d_weight,
+                           size_t rows, size_t cols, float eps, float *d_out);
+/* models/gemma/model.rs:46-51 is_global_layer */
+int spissa_is_global_layer(size_t layer_idx, size_t sliding_window_pattern);
+/* models/gemma/generate.rs:230-278 fused on the device: QK-norm of q and k
+ * rows, Gemma RoPE from `t` (built with the layer's base and divisor), then
+ * q *= q_prescale, with q_prescale = (1/sqrt(query_pre_attn_scalar))*sqrt(head_dim)
+ * as models/gemma/generate.rs:275 computes it. In place. */
+int spissa_gemma_qk_prologue_device(spissa_session *s, const spissa_rope_table *t, float *d_q,
+                                    float *d_k, size_t seq_len, size_t q_heads, size_t kv_heads,
+                                    size_t head_dim, const float *d_q_norm,
+                                    const float *d_k_norm, float eps, size_t position_offset,
+                                    float q_prescale);
+
+/* ------------------------------------------------------------------------ */
+/* Attention                                                                */
+/* ------------------------------------------------------------------------ */
+
+/* rotary.rs:320-327 KvAttentionConfig, extended with a sliding window:
+ * window = 0 is the reference (no window); window = W > 0 additionally masks
+ * keys j with j + W <= i for a query at absolute position i (i-W < j <= i). */
+typedef struct {
+    size_t query_len;
+    size_t num_heads;
+    size_t kv_heads;
+    size_t head_dim;
+    int causal;
+    size_t window;
+} spissa_kv_attention_config;
+
+/* rotary.rs:335-415 scaled_dot_product_attention_with_cache. cache may be NULL
+ * (Option::None). query_len == 1 runs the split-K f32 decode kernel; longer
+ * queries run the bf16-MFMA flash prefill (f32 in and out). out receives
+ * query_len*num_heads*head_dim floats. */
+int spissa_scaled_dot_product_attention_with_cache(const float *q, size_t q_len,
+                                                   const float *current_k, size_t k_len,
+                                                   const float *current_v, size_t v_len,
+                                                   const spissa_kv_cache *cache,
+                                                   const spissa_kv_attention_config *cfg,
+                                                   float *out, size_t out_len);
+/* Same on device buffers, asynchronous on the session stream. */
+int spissa_attention_device(spissa_session *s, const float *d_q, const float *d_k,
+                            const float *d_v, const spissa_kv_cache *cache,
+                            const spissa_kv_attention_config *cfg, float *d_out);
+/* Batched single-token decode over `batch` independent sequences in one
+ * launch (the reference runs one call per sequence). d_q [batch, Hq, d],
+ * d_k/d_v [batch, Hkv, d] (the new token of each sequence), caches[b] holds
+ * sequence b's past; cfg->query_len must be 1. */
+int spissa_attention_decode_batch_device(spissa_session *s, const float *d_q, const float *d_k,
+                                         const float *d_v, const spissa_kv_cache *const *caches,
+                                         size_t batch, const spissa_kv_attention_config *cfg,
+                                         float *d_out);
+/* ops.rs:237-291 scaled_dot_product_attention (cacheless MHA, f32). */
+int spissa_scaled_dot_product_attention(const float *q, size_t q_len, const float *k,
+                                        size_t k_len, const float *v, size_t v_len,
+                                        size_t seq_len, size_t num_heads, size_t head_dim,
+                                        int causal, float *out, size_t out_len);
+
+/* Prefill arithmetic for query_len > 1: SPISSA_PREFILL_BF16 (default) runs
+ * the MFMA kernel; SPISSA_PREFILL_F32 runs the f32 SIMT kernel. */
+typedef enum { SPISSA_PREFILL_BF16 = 0, SPISSA_PREFILL_F32 = 1 } spissa_prefill_precision;
+int spissa_session_set_prefill_precision(spissa_session *s, int precision);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SPISSA_HIP_H */

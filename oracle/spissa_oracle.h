@@ -1,0 +1,118 @@
+/*
+ * spissa_oracle.h -- CPU restatement of the Spissa runtime's attention path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the parity checker for the HIP
+ * path in spissa_amd/: only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load it, and only to check or time the reference
+ * algorithm. The product never links it and never falls back to it.
+ *
+ * Each function restates one function of the Rust reference
+ * (crates/spissa-runtime/src/rotary.rs, crates/spissa-runtime/src/ops.rs,
+ * crates/spissa-runtime/src/models/gemma/{generate,model}.rs) in plain C with
+ * the same loop order and the same f32 operation order. It is compiled with
+ * -fno-fast-math -ffp-contract=off against glibc libm (powf, cosf, sinf, expf,
+ * sqrtf), which is what Rust's f32 methods lower to on x86_64-linux-gnu.
+ *
+ * Status codes mirror RuntimeError variants (crates/spissa-runtime/src/error.rs:6-54):
+ *   0 = Ok, 1 = Shape, 2 = InvalidTensorData.
+ * Where the Rust reference would panic (out-of-range slice index) the oracle
+ * returns Shape instead; no such case is reachable from valid callers.
+ */
+#ifndef SPISSA_ORACLE_H
+#define SPISSA_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { OR_OK = 0, OR_SHAPE = 1, OR_INVALID = 2 };
+
+/* rotary.rs:6-14 */
+typedef struct {
+    size_t seq_len;
+    size_t num_heads;
+    size_t head_dim;
+    size_t rotary_dim;
+    float base;
+    size_t position_offset;
+} or_rotary_config;
+
+/* rotary.rs:320-327, plus the sliding-window extension (window = 0: none). */
+typedef struct {
+    size_t query_len;
+    size_t num_heads;
+    size_t kv_heads;
+    size_t head_dim;
+    int causal;
+    size_t window;
+} or_kv_attention_config;
+
+/* rotary.rs:195-203 */
+typedef struct {
+    size_t num_heads;
+    size_t head_dim;
+    size_t max_seq_len;
+    size_t len;
+    float *keys;   /* capacity max_seq_len * num_heads * head_dim */
+    float *values;
+} or_kv_cache;
+
+const char *or_last_error(void);
+
+int or_gpt_neox_rotary_dim(size_t head_dim, float rotary_pct, size_t *out);
+int or_apply_gpt_neox_rotary_inplace(float *q, size_t q_len, float *k, size_t k_len,
+                                     const or_rotary_config *cfg);
+int or_apply_llama_rotary_inplace(float *q, size_t q_len, float *k, size_t k_len,
+                                  size_t q_heads, size_t k_heads, const or_rotary_config *cfg,
+                                  const float *freq_scale, size_t freq_scale_len);
+int or_apply_gemma_rotary_inplace(float *q, size_t q_len, float *k, size_t k_len,
+                                  size_t q_heads, size_t k_heads, const or_rotary_config *cfg,
+                                  float position_divisor);
+/* Per-(position, pair) cos/sin exactly as rotary.rs computes them, for tables. */
+void or_llama_cos_sin(size_t absolute_pos, size_t pair, size_t rotary_dim, float base,
+                      float freq_scale, float *cos_out, float *sin_out);
+void or_gemma_cos_sin(size_t absolute_pos, size_t pair, size_t rotary_dim, float base,
+                      float position_divisor, float *cos_out, float *sin_out);
+
+or_kv_cache *or_kv_new(size_t num_heads, size_t head_dim, size_t max_seq_len, int *status);
+void or_kv_free(or_kv_cache *c);
+int or_kv_append(or_kv_cache *c, const float *keys, size_t keys_len, const float *values,
+                 size_t values_len, size_t token_count);
+void or_kv_clear(or_kv_cache *c);
+int or_kv_truncate(or_kv_cache *c, size_t len);
+size_t or_kv_resident_bytes(const or_kv_cache *c);
+size_t or_kv_len(const or_kv_cache *c);
+const float *or_kv_keys(const or_kv_cache *c);
+const float *or_kv_values(const or_kv_cache *c);
+
+int or_sdpa_with_cache(const float *q, size_t q_len, const float *cur_k, size_t k_len,
+                       const float *cur_v, size_t v_len, const or_kv_cache *cache,
+                       const or_kv_attention_config *cfg, float *out, size_t out_len);
+
+int or_rms_norm(const float *x, size_t x_len, const float *w, size_t w_len, size_t rows,
+                size_t cols, float eps, float *out);
+int or_softmax_rows(const float *logits, size_t len, size_t rows, size_t cols, float *out);
+int or_scaled_dot_product_attention(const float *q, const float *k, const float *v, size_t len,
+                                    size_t seq_len, size_t num_heads, size_t head_dim,
+                                    int causal, float *out);
+
+int or_is_global_layer(size_t layer_idx, size_t sliding_window_pattern);
+int or_gemma_qk_prologue(float *q, size_t q_len, float *k, size_t k_len, size_t seq_len,
+                         size_t q_heads, size_t kv_heads, size_t head_dim, const float *q_norm,
+                         const float *k_norm, float eps, float rope_base,
+                         float position_divisor, size_t position_offset,
+                         float query_pre_attn_scalar);
+
+/* Harness helper (not part of the reference): runs or_sdpa_with_cache over
+ * `units` independent (cache, q, k, v) sets on `threads` POSIX threads. */
+int or_sdpa_many_threads(size_t units, const float *const *q, const float *const *k,
+                         const float *const *v, const or_kv_cache *const *caches,
+                         const or_kv_attention_config *cfg, float *const *out, int threads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

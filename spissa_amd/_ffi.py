@@ -1,0 +1,154 @@
+"""ctypes binding of include/spissa_hip.h (libspissa_hip.so, built in-tree).
+
+Loading fails loudly when the library has not been built: there is no CPU
+fallback behind this package.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libspissa_hip.so"
+
+OK = 0
+ERR_SHAPE = 1
+ERR_INVALID_TENSOR_DATA = 2
+ERR_DEVICE = 3
+ERR_ARGUMENT = 4
+
+ROPE_LLAMA = 0
+ROPE_GEMMA = 1
+ROPE_NEOX = 2
+
+PREFILL_BF16 = 0
+PREFILL_F32 = 1
+
+c_size = C.c_size_t
+c_float_p = C.POINTER(C.c_float)
+c_void_p = C.c_void_p
+
+
+class RotaryConfigC(C.Structure):
+    """spissa_rotary_config (rotary.rs:6-14)."""
+
+    _fields_ = [
+        ("seq_len", c_size),
+        ("num_heads", c_size),
+        ("head_dim", c_size),
+        ("rotary_dim", c_size),
+        ("base", C.c_float),
+        ("position_offset", c_size),
+    ]
+
+
+class AttnConfigC(C.Structure):
+    """spissa_kv_attention_config (rotary.rs:320-327 + window)."""
+
+    _fields_ = [
+        ("query_len", c_size),
+        ("num_heads", c_size),
+        ("kv_heads", c_size),
+        ("head_dim", c_size),
+        ("causal", C.c_int),
+        ("window", c_size),
+    ]
+
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "spissa_last_error": (C.c_char_p, []),
+    "spissa_version": (C.c_char_p, []),
+    "spissa_session_create": (C.c_int, [C.c_int, c_void_p, C.POINTER(c_void_p)]),
+    "spissa_session_destroy": (None, [c_void_p]),
+    "spissa_default_session": (C.c_int, [C.POINTER(c_void_p)]),
+    "spissa_session_sync": (C.c_int, [c_void_p]),
+    "spissa_session_stream": (c_void_p, [c_void_p]),
+    "spissa_session_device": (C.c_int, [c_void_p]),
+    "spissa_session_set_prefill_precision": (C.c_int, [c_void_p, C.c_int]),
+    "spissa_kv_cache_new": (C.c_int, [c_size, c_size, c_size, C.POINTER(c_void_p)]),
+    "spissa_kv_cache_new_in": (C.c_int, [c_void_p, c_size, c_size, c_size, C.POINTER(c_void_p)]),
+    "spissa_kv_cache_free": (None, [c_void_p]),
+    "spissa_kv_cache_clone": (C.c_int, [c_void_p, C.POINTER(c_void_p)]),
+    "spissa_kv_cache_append": (C.c_int, [c_void_p, c_float_p, c_size, c_float_p, c_size, c_size]),
+    "spissa_kv_cache_append_device": (C.c_int, [c_void_p, c_void_p, c_void_p, c_size]),
+    "spissa_kv_cache_clear": (None, [c_void_p]),
+    "spissa_kv_cache_truncate": (C.c_int, [c_void_p, c_size]),
+    "spissa_kv_cache_len": (c_size, [c_void_p]),
+    "spissa_kv_cache_is_empty": (C.c_int, [c_void_p]),
+    "spissa_kv_cache_max_seq_len": (c_size, [c_void_p]),
+    "spissa_kv_cache_num_heads": (c_size, [c_void_p]),
+    "spissa_kv_cache_head_dim": (c_size, [c_void_p]),
+    "spissa_kv_cache_resident_bytes": (c_size, [c_void_p]),
+    "spissa_kv_cache_read_keys": (C.c_int, [c_void_p, c_float_p, c_size]),
+    "spissa_kv_cache_read_values": (C.c_int, [c_void_p, c_float_p, c_size]),
+    "spissa_kv_cache_device_keys": (c_void_p, [c_void_p]),
+    "spissa_kv_cache_device_values": (c_void_p, [c_void_p]),
+    "spissa_gpt_neox_rotary_dim": (C.c_int, [c_size, C.c_float, C.POINTER(c_size)]),
+    "spissa_apply_gpt_neox_rotary_inplace": (
+        C.c_int, [c_float_p, c_size, c_float_p, c_size, C.POINTER(RotaryConfigC)]),
+    "spissa_apply_llama_rotary_inplace": (
+        C.c_int,
+        [c_float_p, c_size, c_float_p, c_size, c_size, c_size, C.POINTER(RotaryConfigC), c_float_p,
+         c_size]),
+    "spissa_apply_gemma_rotary_inplace": (
+        C.c_int,
+        [c_float_p, c_size, c_float_p, c_size, c_size, c_size, C.POINTER(RotaryConfigC), C.c_float]),
+    "spissa_rope_table_new": (
+        C.c_int,
+        [c_void_p, C.c_int, c_size, C.c_float, C.c_float, c_float_p, c_size, c_size,
+         C.POINTER(c_void_p)]),
+    "spissa_rope_table_free": (None, [c_void_p]),
+    "spissa_rope_apply_device": (
+        C.c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size, c_size, c_size, c_size, c_size]),
+    "spissa_rms_norm": (
+        C.c_int, [c_float_p, c_size, c_float_p, c_size, c_size, c_size, C.c_float, c_float_p, c_size]),
+    "spissa_rms_norm_device": (
+        C.c_int, [c_void_p, c_void_p, c_void_p, c_size, c_size, C.c_float, c_void_p]),
+    "spissa_is_global_layer": (C.c_int, [c_size, c_size]),
+    "spissa_gemma_qk_prologue_device": (
+        C.c_int,
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_size, c_size, c_size, c_size, c_void_p, c_void_p,
+         C.c_float, c_size, C.c_float]),
+    "spissa_scaled_dot_product_attention_with_cache": (
+        C.c_int,
+        [c_float_p, c_size, c_float_p, c_size, c_float_p, c_size, c_void_p, C.POINTER(AttnConfigC),
+         c_float_p, c_size]),
+    "spissa_attention_device": (
+        C.c_int,
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, C.POINTER(AttnConfigC), c_void_p]),
+    "spissa_attention_decode_batch_device": (
+        C.c_int,
+        [c_void_p, c_void_p, c_void_p, c_void_p, C.POINTER(c_void_p), c_size,
+         C.POINTER(AttnConfigC), c_void_p]),
+    "spissa_scaled_dot_product_attention": (
+        C.c_int,
+        [c_float_p, c_size, c_float_p, c_size, c_float_p, c_size, c_size, c_size, c_size, C.c_int,
+         c_float_p, c_size]),
+}
+
+_lib = None
+
+
+def load() -> C.CDLL:
+    """Loads libspissa_hip.so; raises ImportError with the build command when absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = Path(os.environ.get("SPISSA_HIP_LIB", LIB_PATH))
+    if not path.exists():
+        raise ImportError(
+            f"{path} is missing: build the HIP extension first (python -m spissa_amd.build); "
+            "spissa_amd has no CPU fallback")
+    lib = C.CDLL(str(path), mode=C.RTLD_GLOBAL)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def last_error() -> str:
+    msg = load().spissa_last_error()
+    return msg.decode() if msg else ""

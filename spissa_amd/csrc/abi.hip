@@ -1,0 +1,1066 @@
+// abi.hip -- the extern "C" boundary (include/spissa_hip.h): sessions, the
+// device-resident KV cache, validation with the reference's error contract,
+// host-side RoPE tables, and dispatch to the gfx950 kernels.
+//
+// Validation order and messages follow crates/spissa-runtime/src/rotary.rs
+// and ops.rs so that a caller sees the same RuntimeError variant for the same
+// bad input; every check runs before anything is mutated.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <new>
+#include <thread>
+#include <vector>
+
+#include "internal.hpp"
+
+using namespace spissa;
+
+// ------------------------------------------------------------------------
+// errors
+// ------------------------------------------------------------------------
+static thread_local char g_err[1024];
+
+static int set_err(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+#define HIP_TRY(expr)                                                                       \
+  do {                                                                                      \
+    hipError_t e_ = (expr);                                                                 \
+    if (e_ != hipSuccess)                                                                   \
+      return set_err(SPISSA_ERR_DEVICE, "%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_), \
+                     __FILE__, __LINE__);                                                   \
+  } while (0)
+
+#define GUARD_BEGIN try {
+#define GUARD_END                                                                 \
+  }                                                                               \
+  catch (const std::bad_alloc &) {                                                \
+    return set_err(SPISSA_ERR_DEVICE, "host allocation failed");                  \
+  }                                                                               \
+  catch (...) {                                                                   \
+    return set_err(SPISSA_ERR_DEVICE, "unexpected C++ exception at the C boundary"); \
+  }
+
+static bool mul_ovf(size_t a, size_t b, size_t *out) { return __builtin_mul_overflow(a, b, out); }
+
+extern "C" const char *spissa_last_error(void) { return g_err; }
+extern "C" const char *spissa_version(void) { return "spissa-hip 0.1.0 (gfx950)"; }
+
+// ------------------------------------------------------------------------
+// sessions and workspace
+// ------------------------------------------------------------------------
+struct DevBuf {
+  void *p = nullptr;
+  size_t bytes = 0;
+};
+
+struct spissa_session {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  bool own_stream = false;
+  int *d_err = nullptr;
+  DevBuf io;        // drop-in host<->device staging
+  DevBuf partial;   // decode combine-tree entries
+  DevBuf counters;  // decode combine-tree counters (kept zero between launches)
+  DevBuf stage;     // prefill bf16 staging of K / V^T
+  DevBuf table;     // drop-in RoPE rows
+  int prefill_precision = SPISSA_PREFILL_BF16;
+};
+
+struct spissa_kv_cache {
+  spissa_session *session = nullptr;
+  size_t num_heads = 0, head_dim = 0, max_seq_len = 0, len = 0;
+  float *keys = nullptr;    // [max_seq_len, H, D]
+  float *values = nullptr;  // [max_seq_len, H, D]
+  bf16 *kb = nullptr;       // bf16 shadow [H, cap, D], allocated at first prefill use
+  bf16 *vt = nullptr;       // bf16 shadow [H, D, cap]
+  size_t shadow_cap = 0;
+  size_t width() const { return num_heads * head_dim; }
+};
+
+struct spissa_rope_table {
+  int device = 0;
+  int kind = 0;
+  size_t rotary_dim = 0, half = 0, max_positions = 0;
+  float *cos = nullptr, *sin = nullptr;  // [max_positions, half]
+};
+
+static int ensure_buf(spissa_session *s, DevBuf &b, size_t bytes, bool zero) {
+  if (bytes <= b.bytes) return SPISSA_OK;
+  size_t want = std::max(bytes, b.bytes + b.bytes / 2);
+  want = (want + 4095) & ~(size_t)4095;
+  HIP_TRY(hipSetDevice(s->device));
+  if (b.p) {
+    HIP_TRY(hipStreamSynchronize(s->stream));
+    HIP_TRY(hipFree(b.p));
+    b.p = nullptr;
+    b.bytes = 0;
+  }
+  HIP_TRY(hipMalloc(&b.p, want));
+  if (zero) {
+    HIP_TRY(hipMemsetAsync(b.p, 0, want, s->stream));
+    HIP_TRY(hipStreamSynchronize(s->stream));
+  }
+  b.bytes = want;
+  return SPISSA_OK;
+}
+
+static void free_buf(DevBuf &b) {
+  if (b.p) (void)hipFree(b.p);
+  b.p = nullptr;
+  b.bytes = 0;
+}
+
+extern "C" int spissa_session_create(int device, void *stream, spissa_session **out) {
+  GUARD_BEGIN
+  if (!out) return set_err(SPISSA_ERR_ARGUMENT, "out is null");
+  *out = nullptr;
+  int n = 0;
+  HIP_TRY(hipGetDeviceCount(&n));
+  if (device < 0 || device >= n) return set_err(SPISSA_ERR_DEVICE, "device %d not present (%d)", device, n);
+  HIP_TRY(hipSetDevice(device));
+  std::unique_ptr<spissa_session> s(new spissa_session());
+  s->device = device;
+  if (stream) {
+    s->stream = (hipStream_t)stream;
+  } else {
+    HIP_TRY(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking));
+    s->own_stream = true;
+  }
+  HIP_TRY(hipMalloc(&s->d_err, sizeof(int)));
+  HIP_TRY(hipMemsetAsync(s->d_err, 0, sizeof(int), s->stream));
+  HIP_TRY(hipStreamSynchronize(s->stream));
+  *out = s.release();
+  return SPISSA_OK;
+  GUARD_END
+}
+
+extern "C" void spissa_session_destroy(spissa_session *s) {
+  if (!s) return;
+  (void)hipSetDevice(s->device);
+  (void)hipStreamSynchronize(s->stream);
+  free_buf(s->io);
+  free_buf(s->partial);
+  free_buf(s->counters);
+  free_buf(s->stage);
+  free_buf(s->table);
+  if (s->d_err) (void)hipFree(s->d_err);
+  if (s->own_stream) (void)hipStreamDestroy(s->stream);
+  delete s;
+}
+
+namespace {
+struct DefaultSessions {
+  std::vector<spissa_session *> by_device;
+  ~DefaultSessions() {
+    for (auto *s : by_device) spissa_session_destroy(s);
+  }
+};
+thread_local DefaultSessions t_default;
+}  // namespace
+
+extern "C" int spissa_default_session(spissa_session **out) {
+  GUARD_BEGIN
+  if (!out) return set_err(SPISSA_ERR_ARGUMENT, "out is null");
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  if ((int)t_default.by_device.size() <= dev) t_default.by_device.resize(dev + 1, nullptr);
+  if (!t_default.by_device[dev]) {
+    int st = spissa_session_create(dev, nullptr, &t_default.by_device[dev]);
+    if (st) return st;
+  }
+  *out = t_default.by_device[dev];
+  return SPISSA_OK;
+  GUARD_END
+}
+
+extern "C" int spissa_session_sync(spissa_session *s) {
+  GUARD_BEGIN
+  if (!s) return set_err(SPISSA_ERR_ARGUMENT, "session is null");
+  HIP_TRY(hipSetDevice(s->device));
+  HIP_TRY(hipStreamSynchronize(s->stream));
+  int flag = 0;
+  HIP_TRY(hipMemcpy(&flag, s->d_err, sizeof(int), hipMemcpyDeviceToHost));
+  if (flag) {
+    HIP_TRY(hipMemsetAsync(s->d_err, 0, sizeof(int), s->stream));
+    HIP_TRY(hipStreamSynchronize(s->stream));
+    if (flag & kDevErrSoftmaxDenominator)
+      return set_err(SPISSA_ERR_INVALID_TENSOR_DATA, "softmax produced invalid denominator");
+    return set_err(SPISSA_ERR_DEVICE, "device error flag 0x%x", flag);
+  }
+  return SPISSA_OK;
+  GUARD_END
+}
+
+extern "C" void *spissa_session_stream(spissa_session *s) { return s ? (void *)s->stream : nullptr; }
+extern "C" int spissa_session_device(const spissa_session *s) { return s ? s->device : -1; }
+
+extern "C" int spissa_session_set_prefill_precision(spissa_session *s, int precision) {
+  if (!s) return set_err(SPISSA_ERR_ARGUMENT, "session is null");
+  if (precision != SPISSA_PREFILL_BF16 && precision != SPISSA_PREFILL_F32)
+    return set_err(SPISSA_ERR_ARGUMENT, "unknown prefill precision %d", precision);
+  s->prefill_precision = precision;
+  return SPISSA_OK;
+}
+
+// Host-buffer staging for drop-in calls: carve `n` float regions out of s->io.
+static int io_regions(spissa_session *s, std::initializer_list<size_t> sizes, float **out) {
+  size_t total = 0;
+  for (size_t n : sizes) total += (n + 63) & ~(size_t)63;
+  int st = ensure_buf(s, s->io, std::max<size_t>(total, 64) * sizeof(float), false);
+  if (st) return st;
+  float *p = (float *)s->io.p;
+  int i = 0;
+  for (size_t n : sizes) {
+    out[i++] = p;
+    p += (n + 63) & ~(size_t)63;
+  }
+  return SPISSA_OK;
+}
+
+static int h2d(spissa_session *s, void *dst, const void *src, size_t bytes) {
+  if (bytes == 0) return SPISSA_OK;
+  HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s->stream));
+  return SPISSA_OK;
+}
+static int d2h(spissa_session *s, void *dst, const void *src, size_t bytes) {
+  if (bytes == 0) return SPISSA_OK;
+  HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s->stream));
+  return SPISSA_OK;
+}
+static int sync_stream(spissa_session *s) {
+  HIP_TRY(hipStreamSynchronize(s->stream));
+  return SPISSA_OK;
+}
+
+#define ST_TRY(expr)        \
+  do {                      \
+    int st_ = (expr);       \
+    if (st_) return st_;    \
+  } while (0)
+
+// ------------------------------------------------------------------------
+// KV cache (rotary.rs:195-318)
+// ------------------------------------------------------------------------
+static int kv_validate_new(size_t num_heads, size_t head_dim, size_t max_seq_len) {
+  // rotary.rs:207-215
+  if (num_heads == 0 || head_dim == 0 || max_seq_len == 0)
+    return set_err(SPISSA_ERR_SHAPE,
+                   "KV cache dimensions must be non-zero, got num_heads=%zu, head_dim=%zu, "
+                   "max_seq_len=%zu",
+                   num_heads, head_dim, max_seq_len);
+  size_t cap;
+  if (mul_ovf(max_seq_len, num_heads, &cap) || mul_ovf(cap, head_dim, &cap) ||
+      cap > ((size_t)1 << 61) / sizeof(float))
+    return set_err(SPISSA_ERR_SHAPE, "KV cache capacity overflow");
+  return SPISSA_OK;
+}
+
+static int kv_new_impl(spissa_session *s, size_t num_heads, size_t head_dim, size_t max_seq_len,
+                       spissa_kv_cache **out) {
+  if (!out) return set_err(SPISSA_ERR_ARGUMENT, "out is null");
+  *out = nullptr;
+  // rotary.rs:207-211
+  if (num_heads == 0 || head_dim == 0 || max_seq_len == 0)
+    return set_err(SPISSA_ERR_SHAPE,
+                   "KV cache dimensions must be non-zero, got num_heads=%zu, head_dim=%zu, "
+                   "max_seq_len=%zu",
+                   num_heads, head_dim, max_seq_len);
+  // rotary.rs:212-215
+  size_t cap;
+  if (mul_ovf(max_seq_len, num_heads, &cap) || mul_ovf(cap, head_dim, &cap) ||
+      cap > ((size_t)1 << 61) / sizeof(float))
+    return set_err(SPISSA_ERR_SHAPE, "KV cache capacity overflow");
+  std::unique_ptr<spissa_kv_cache> c(new spissa_kv_cache());
+  c->session = s;
+  c->num_heads = num_heads;
+  c->head_dim = head_dim;
+  c->max_seq_len = max_seq_len;
+  HIP_TRY(hipSetDevice(s->device));
+  HIP_TRY(hipMalloc(&c->keys, cap * sizeof(float)));
+  hipError_t e = hipMalloc(&c->values, cap * sizeof(float));
+  if (e != hipSuccess) {
+    (void)hipFree(c->keys);
+    return set_err(SPISSA_ERR_DEVICE, "hipMalloc of %zu bytes failed: %s", cap * sizeof(float),
+                   hipGetErrorString(e));
+  }
+  *out = c.release();
+  return SPISSA_OK;
+}
+
+extern "C" int spissa_kv_cache_new_in(spissa_session *s, size_t num_heads, size_t head_dim,
+                                      size_t max_seq_len, spissa_kv_cache **out) {
+  GUARD_BEGIN
+  if (!s) return set_err(SPISSA_ERR_ARGUMENT, "session is null");
+  return kv_new_impl(s, num_heads, head_dim, max_seq_len, out);
+  GUARD_END
+}
+
+extern "C" int spissa_kv_cache_new(size_t num_heads, size_t head_dim, size_t max_seq_len,
+                                   spissa_kv_cache **out) {
+  GUARD_BEGIN
+  if (!out) return set_err(SPISSA_ERR_ARGUMENT, "out is null");
+  *out = nullptr;
+  ST_TRY(kv_validate_new(num_heads, head_dim, max_seq_len));
+  spissa_session *s = nullptr;
+  ST_TRY(spissa_default_session(&s));
+  return kv_new_impl(s, num_heads, head_dim, max_seq_len, out);
+  GUARD_END
+}
+
+static void kv_release(spissa_kv_cache *c) {
+  (void)hipSetDevice(c->session->device);
+  (void)hipStreamSynchronize(c->session->stream);
+  if (c->keys) (void)hipFree(c->keys);
+  if (c->values) (void)hipFree(c->values);
+  if (c->kb) (void)hipFree(c->kb);
+  if (c->vt) (void)hipFree(c->vt);
+}
+
+extern "C" void spissa_kv_cache_free(spissa_kv_cache *c) {
+  if (!c) return;
+  kv_release(c);
+  delete c;
+}
+
+// Converts rows [first, first + n) of the cache into the bf16 shadow, on `st`.
+static int shadow_update(spissa_kv_cache *c, size_t first, size_t n, hipStream_t st) {
+  if (!c->kb || n == 0) return SPISSA_OK;
+  const size_t w = c->width();
+  HIP_TRY(launch_stage_bf16(st, c->keys + first * w, c->values + first * w, n, n, c->num_heads, c->head_dim,
+                            c->kb, c->vt, first, c->shadow_cap));
+  return SPISSA_OK;
+}
+
+// Allocates the bf16 shadow on first prefill use and converts rows [0, len) on `st`.
+static int ensure_shadow(spissa_kv_cache *c, hipStream_t st) {
+  if (c->kb) return SPISSA_OK;
+  const size_t cap = (c->max_seq_len + 63) & ~(size_t)63;
+  const size_t elems = cap * c->width();
+  HIP_TRY(hipSetDevice(c->session->device));
+  HIP_TRY(hipMalloc(&c->kb, elems * sizeof(bf16)));
+  hipError_t e = hipMalloc(&c->vt, elems * sizeof(bf16));
+  if (e != hipSuccess) {
+    (void)hipFree(c->kb);
+    c->kb = nullptr;
+    return set_err(SPISSA_ERR_DEVICE, "hipMalloc of the bf16 shadow failed: %s", hipGetErrorString(e));
+  }
+  c->shadow_cap = cap;
+  return shadow_update(c, 0, c->len, st);
+}
+
+static int kv_validate_append(const spissa_kv_cache *c, size_t keys_len, size_t values_len,
+                              size_t token_count, bool check_lens, size_t *n_out, size_t *new_len) {
+  // rotary.rs:227-251, in the same order.
+  if (token_count == 0)
+    return set_err(SPISSA_ERR_SHAPE, "KV cache append token_count must be greater than zero");
+  size_t n;
+  if (mul_ovf(token_count, c->width(), &n)) return set_err(SPISSA_ERR_SHAPE, "KV append length overflow");
+  if (check_lens && (keys_len != n || values_len != n))
+    return set_err(SPISSA_ERR_SHAPE, "KV append shape mismatch: expected %zu, got keys=%zu, values=%zu", n,
+                   keys_len, values_len);
+  size_t nl;
+  if (__builtin_add_overflow(c->len, token_count, &nl)) return set_err(SPISSA_ERR_SHAPE, "KV cache length overflow");
+  if (nl > c->max_seq_len)
+    return set_err(SPISSA_ERR_SHAPE, "KV cache capacity exceeded: append would set len %zu, max_seq_len %zu",
+                   nl, c->max_seq_len);
+  *n_out = n;
+  *new_len = nl;
+  return SPISSA_OK;
+}
+
+extern "C" int spissa_kv_cache_append(spissa_kv_cache *c, const float *keys, size_t keys_len,
+                                      const float *values, size_t values_len, size_t token_count) {
+  GUARD_BEGIN
+  if (!c) return set_err(SPISSA_ERR_ARGUMENT, "cache is null");
+  size_t n, nl;
+  ST_TRY(kv_validate_append(c, keys_len, values_len, token_count, true, &n, &nl));
+  if (!keys || !values) return set_err(SPISSA_ERR_ARGUMENT, "keys/values are null");
+  spissa_session *s = c->session;
+  HIP_TRY(hipSetDevice(s->device));
+  const size_t off = c->len * c->width();
+  ST_TRY(h2d(s, c->keys + off, keys, n * sizeof(float)));
+  ST_TRY(h2d(s, c->values + off, values, n * sizeof(float)));
+  ST_TRY(shadow_update(c, c->len, token_count, s->stream));
+  ST_TRY(sync_stream(s));
+  c->len = nl;
+  return SPISSA_OK;
+  GUARD_END
+}
+
+extern "C" int spissa_kv_cache_append_device(spissa_kv_cache *c, const float *d_keys,
+                                             const float *d_values, size_t token_count) {
+  GUARD_BEGIN
+  if (!c) return set_err(SPISSA_ERR_ARGUMENT, "cache is null");
+  size_t n, nl;
+  ST_TRY(kv_validate_append(c, 0, 0, token_count, false, &n, &nl));
+  if (!d_keys || !d_values) return set_err(SPISSA_ERR_ARGUMENT, "keys/values are null");
+  spissa_session *s = c->session;
+  HIP_TRY(hipSetDevice(s->device));
+  const size_t off = c->len * c->width();
+  HIP_TRY(hipMemcpyAsync(c->keys + off, d_keys, n * sizeof(float), hipMemcpyDeviceToDevice, s->stream));
+  HIP_TRY(hipMemcpyAsync(c->values + off, d_values, n * sizeof(float), hipMemcpyDeviceToDevice, s->stream));
+  ST_TRY(shadow_update(c, c->len, token_count, s->stream));
+  c->len = nl;
+  return SPISSA_OK;
+  GUARD_END
+}
+
+extern "C" void spissa_kv_cache_clear(spissa_kv_cache *c) {
+  if (c) c->len = 0;
+}
+
+extern "C" int spissa_kv_cache_truncate(spissa_kv_cache *c, size_t len) {
+  if (!c) return set_err(SPISSA_ERR_ARGUMENT, "cache is null");
+  // rotary.rs:264-278
+  if (len > c->len) return set_err(SPISSA_ERR_SHAPE, "KV cache truncate cannot grow from %zu to %zu", c->len, len);
+  size_t v;
+  if (mul_ovf(len, c->width(), &v)) return set_err(SPISSA_ERR_SHAPE, "KV truncate length overflow");
+  c->len = len;
+  return SPISSA_OK;
+}
+
+extern "C" size_t spissa_kv_cache_len(const spissa_kv_cache *c) { return c ? c->len : 0; }
+extern "C" int spissa_kv_cache_is_empty(const spissa_kv_cache *c) { return c ? c->len == 0 : 1; }
+extern "C" size_t spissa_kv_cache_max_seq_len(const spissa_kv_cache *c) { return c ? c->max_seq_len : 0; }
+extern "C" size_t spissa_kv_cache_num_heads(const spissa_kv_cache *c) { return c ? c->num_heads : 0; }
+extern "C" size_t spissa_kv_cache_head_dim(const spissa_kv_cache *c) { return c ? c->head_dim : 0; }
+
+// rotary.rs:280-285 (saturating multiply)
+extern "C" size_t spissa_kv_cache_resident_bytes(const spissa_kv_cache *c) {
+  if (!c) return 0;
+  size_t r;
+  if (mul_ovf(c->len, c->width(), &r) || mul_ovf(r, 2, &r) || mul_ovf(r, sizeof(float), &r))
+    return (size_t)-1;
+  return r;
+}
+
+static int kv_read(const spissa_kv_cache *c, const float *src, float *dst, size_t dst_len) {
+  if (!c) return set_err(SPISSA_ERR_ARGUMENT, "cache is null");
+  const size_t n = c->len * c->width();
+  if (dst_len < n) return set_err(SPISSA_ERR_SHAPE, "destination holds %zu floats, cache has %zu", dst_len, n);
+  if (n == 0) return SPISSA_OK;
+  if (!dst) return set_err(SPISSA_ERR_ARGUMENT, "dst is null");
+  spissa_session *s = c->session;
+  HIP_TRY(hipSetDevice(s->device));
+  ST_TRY(d2h(s, dst, src, n * sizeof(float)));
+  return sync_stream(s);
+}
+
+extern "C" int spissa_kv_cache_read_keys(const spissa_kv_cache *c, float *dst, size_t dst_len) {
+  GUARD_BEGIN
+  return kv_read(c, c ? c->keys : nullptr, dst, dst_len);
+  GUARD_END
+}
+extern "C" int spissa_kv_cache_read_values(const spissa_kv_cache *c, float *dst, size_t dst_len) {
+  GUARD_BEGIN
+  return kv_read(c, c ? c->values : nullptr, dst, dst_len);
+  GUARD_END
+}
+extern "C" const float *spissa_kv_cache_device_keys(const spissa_kv_cache *c) { return c ? c->keys : nullptr; }
+extern "C" const float *spissa_kv_cache_device_values(const spissa_kv_cache *c) { return c ? c->values : nullptr; }
+
+extern "C" int spissa_kv_cache_clone(const spissa_kv_cache *c, spissa_kv_cache **out) {
+  GUARD_BEGIN
+  if (!c || !out) return set_err(SPISSA_ERR_ARGUMENT, "null argument");
+  spissa_kv_cache *n = nullptr;
+  ST_TRY(kv_new_impl(c->session, c->num_heads, c->head_dim, c->max_seq_len, &n));
+  spissa_session *s = c->session;
+  const size_t bytes = c->len * c->width() * sizeof(float);
+  hipError_t e = hipSuccess;
+  if (bytes) {
+    e = hipMemcpyAsync(n->keys, c->keys, bytes, hipMemcpyDeviceToDevice, s->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(n->values, c->values, bytes, hipMemcpyDeviceToDevice, s->stream);
+  }
+  if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+  if (e != hipSuccess) {
+    spissa_kv_cache_free(n);
+    return set_err(SPISSA_ERR_DEVICE, "clone copy failed: %s", hipGetErrorString(e));
+  }
+  n->len = c->len;
+  *out = n;
+  return SPISSA_OK;
+  GUARD_END
+}
+
+// ------------------------------------------------------------------------
+// RoPE (rotary.rs:6-193)
+// ------------------------------------------------------------------------
+namespace {
+
+#pragma clang fp contract(off)
+// rotary.rs:454-465 rotary_angle -> cos/sin (llama and gpt-neox kinds).
+inline void llama_cos_sin(size_t abs_pos, float inv_freq, float *c, float *s) {
+  const float angle = (float)abs_pos * inv_freq;
+  *c = cosf(angle);
+  *s = sinf(angle);
+}
+inline float llama_inv_freq(size_t pair, size_t rotary_dim, float base, float scale) {
+  const float exponent = (float)(2 * pair) / (float)rotary_dim;
+  return 1.0f / (powf(base, exponent) * scale);
+}
+// rotary.rs:168 and 188-193 (gemma kind).
+inline float gemma_inv_freq(size_t pair, size_t rotary_dim, float base) {
+  const float exponent = (float)(2 * pair) / (float)rotary_dim;
+  return 1.0f / powf(base, exponent);
+}
+inline void gemma_cos_sin(size_t abs_pos, float divisor, float inv_freq, float *c, float *s) {
+  const float scaled_pos = (float)abs_pos / divisor;
+  const float angle = scaled_pos * inv_freq;
+  *c = cosf(angle);
+  *s = sinf(angle);
+}
+#pragma clang fp contract(on)
+
+// Fills cos/sin [n_pos][half] for absolute positions first .. first + n_pos.
+void fill_table(int kind, size_t rotary_dim, size_t half, float base, float divisor,
+                const float *freq_scale, size_t freq_scale_len, size_t first, size_t n_pos,
+                float *cos_out, float *sin_out) {
+  std::vector<float> inv(half);
+  for (size_t p = 0; p < half; ++p) {
+    if (kind == SPISSA_ROPE_GEMMA) {
+      inv[p] = gemma_inv_freq(p, rotary_dim, base);
+    } else {
+      const float scale =
+          (kind == SPISSA_ROPE_LLAMA && freq_scale && p < freq_scale_len) ? freq_scale[p] : 1.0f;
+      inv[p] = llama_inv_freq(p, rotary_dim, base, scale);
+    }
+  }
+  auto work = [&](size_t r0, size_t r1) {
+    for (size_t r = r0; r < r1; ++r)
+      for (size_t p = 0; p < half; ++p) {
+        float c, s;
+        if (kind == SPISSA_ROPE_GEMMA)
+          gemma_cos_sin(first + r, divisor, inv[p], &c, &s);
+        else
+          llama_cos_sin(first + r, inv[p], &c, &s);
+        cos_out[r * half + p] = c;
+        sin_out[r * half + p] = s;
+      }
+  };
+  const size_t total = n_pos * half;
+  unsigned nt = total > (1u << 16) ? std::min(16u, std::max(1u, std::thread::hardware_concurrency())) : 1u;
+  if (nt <= 1) {
+    work(0, n_pos);
+    return;
+  }
+  std::vector<std::thread> ts;
+  size_t per = (n_pos + nt - 1) / nt;
+  for (unsigned t = 0; t < nt; ++t) {
+    size_t a = t * per, b = std::min(n_pos, a + per);
+    if (a < b) ts.emplace_back(work, a, b);
+  }
+  for (auto &t : ts) t.join();
+}
+
+// Runs RoPE on host q/k through the device kernel with a per-call table.
+int rope_dropin(int kind, float *q, size_t q_len, float *k, size_t k_len, size_t qh, size_t kh,
+                const spissa_rotary_config *cfg, float divisor, const float *fs, size_t fs_len) {
+  spissa_session *s = nullptr;
+  ST_TRY(spissa_default_session(&s));
+  const size_t half = cfg->rotary_dim / 2;
+  const size_t S = cfg->seq_len;
+  if (S == 0 || half == 0 || (q_len == 0 && k_len == 0)) return SPISSA_OK;
+  std::vector<float> cs(S * half), sn(S * half);
+  fill_table(kind, cfg->rotary_dim, half, cfg->base, divisor, fs, fs_len, cfg->position_offset, S,
+             cs.data(), sn.data());
+  float *r[4];
+  ST_TRY(io_regions(s, {q_len, k_len, S * half, S * half}, r));
+  HIP_TRY(hipSetDevice(s->device));
+  ST_TRY(h2d(s, r[0], q, q_len * sizeof(float)));
+  ST_TRY(h2d(s, r[1], k, k_len * sizeof(float)));
+  ST_TRY(h2d(s, r[2], cs.data(), cs.size() * sizeof(float)));
+  ST_TRY(h2d(s, r[3], sn.data(), sn.size() * sizeof(float)));
+  HIP_TRY(launch_rope_apply(s->stream, r[2], r[3], half, r[0], r[1], S, qh, kh, cfg->head_dim, half));
+  ST_TRY(d2h(s, q, r[0], q_len * sizeof(float)));
+  ST_TRY(d2h(s, k, r[1], k_len * sizeof(float)));
+  return sync_stream(s);
+}
+
+// The reference indexes past the head row when 2*(rotary_dim/2) > head_dim
+// (a slice panic, or a write into the next head); this ABI reports Shape.
+int guard_half(const spissa_rotary_config *cfg) {
+  if (cfg->seq_len > 0 && 2 * (cfg->rotary_dim / 2) > cfg->head_dim)
+    return set_err(SPISSA_ERR_SHAPE, "rotary_dim %zu exceeds head_dim %zu", cfg->rotary_dim, cfg->head_dim);
+  return SPISSA_OK;
+}
+
+}  // namespace
+
+extern "C" int spissa_gpt_neox_rotary_dim(size_t head_dim, float rotary_pct, size_t *out) {
+  // rotary.rs:17-38
+  if (!out) return set_err(SPISSA_ERR_ARGUMENT, "out is null");
+  if (head_dim == 0) return set_err(SPISSA_ERR_SHAPE, "head_dim must be greater than zero");
+  if (!std::isfinite(rotary_pct) || rotary_pct <= 0.0f || rotary_pct > 1.0f)
+    return set_err(SPISSA_ERR_INVALID_TENSOR_DATA, "rotary_pct must be finite and in (0, 1], got %g", rotary_pct);
+  const float prod = (float)head_dim * rotary_pct;
+  size_t dim = (size_t)prod;
+  if (dim % 2 != 0) dim -= 1;
+  if (dim == 0)
+    return set_err(SPISSA_ERR_SHAPE, "rotary_pct %g produces zero even rotary dim for head_dim %zu", rotary_pct,
+                   head_dim);
+  *out = dim;
+  return SPISSA_OK;
+}
+
+extern "C" int spissa_apply_gpt_neox_rotary_inplace(float *q, size_t q_len, float *k, size_t k_len,
+                                                    const spissa_rotary_config *cfg) {
+  GUARD_BEGIN
+  if (!cfg) return set_err(SPISSA_ERR_ARGUMENT, "config is null");
+  // rotary.rs:417-452 validate_rotary_inputs
+  size_t expected;
+  if (mul_ovf(cfg->seq_len, cfg->num_heads, &expected) || mul_ovf(expected, cfg->head_dim, &expected))
+    return set_err(SPISSA_ERR_SHAPE, "rotary input length overflow");
+  if (q_len != expected || k_len != expected)
+    return set_err(SPISSA_ERR_SHAPE, "rotary Q/K shape mismatch: expected %zu, got q=%zu, k=%zu", expected, q_len,
+                   k_len);
+  if (cfg->seq_len == 0 || cfg->num_heads == 0 || cfg->head_dim == 0)
+    return set_err(SPISSA_ERR_SHAPE, "rotary dimensions must be non-zero, got seq_len=%zu, num_heads=%zu, head_dim=%zu",
+                   cfg->seq_len, cfg->num_heads, cfg->head_dim);
+  if (cfg->rotary_dim == 0 || cfg->rotary_dim > cfg->head_dim || cfg->rotary_dim % 2 != 0)
+    return set_err(SPISSA_ERR_SHAPE, "rotary_dim must be even and in 1..=head_dim, got rotary_dim=%zu, head_dim=%zu",
+                   cfg->rotary_dim, cfg->head_dim);
+  if (!std::isfinite(cfg->base) || cfg->base <= 0.0f)
+    return set_err(SPISSA_ERR_INVALID_TENSOR_DATA, "rotary base must be finite and positive, got %g", cfg->base);
+  size_t last;
+  if (__builtin_add_overflow(cfg->position_offset, cfg->seq_len - 1, &last))
+    return set_err(SPISSA_ERR_SHAPE, "rotary absolute position overflow");
+  if (!q || !k) return set_err(SPISSA_ERR_ARGUMENT, "q/k are null");
+  return rope_dropin(SPISSA_ROPE_NEOX, q, q_len, k, k_len, cfg->num_heads, cfg->num_heads, cfg, 1.0f,
+                     nullptr, 0);
+  GUARD_END
+}
+
+extern "C" int spissa_apply_llama_rotary_inplace(float *q, size_t q_len, float *k, size_t k_len,
+                                                 size_t q_heads, size_t k_heads,
+                                                 const spissa_rotary_config *cfg,
+                                                 const float *freq_scale, size_t freq_scale_len) {
+  GUARD_BEGIN
+  if (!cfg) return set_err(SPISSA_ERR_ARGUMENT, "config is null");
+  // rotary.rs:83-96
+  if (q_heads == 0 || k_heads == 0) return set_err(SPISSA_ERR_SHAPE, "heads must be > 0");
+  const size_t eq = cfg->seq_len * q_heads * cfg->head_dim;
+  const size_t ek = cfg->seq_len * k_heads * cfg->head_dim;
+  if (q_len != eq || k_len != ek)
+    return set_err(SPISSA_ERR_SHAPE, "rotary shape mismatch: q=%zu, expected=%zu, k=%zu, expected=%zu", q_len, eq,
+                   k_len, ek);
+  ST_TRY(guard_half(cfg));
+  if ((!q && q_len) || (!k && k_len)) return set_err(SPISSA_ERR_ARGUMENT, "q/k are null");
+  return rope_dropin(SPISSA_ROPE_LLAMA, q, q_len, k, k_len, q_heads, k_heads, cfg, 1.0f, freq_scale,
+                     freq_scale ? freq_scale_len : 0);
+  GUARD_END
+}
+
+extern "C" int spissa_apply_gemma_rotary_inplace(float *q, size_t q_len, float *k, size_t k_len,
+                                                 size_t q_heads, size_t k_heads,
+                                                 const spissa_rotary_config *cfg,
+                                                 float position_divisor) {
+  GUARD_BEGIN
+  if (!cfg) return set_err(SPISSA_ERR_ARGUMENT, "config is null");
+  // rotary.rs:145-163
+  if (q_heads == 0 || k_heads == 0) return set_err(SPISSA_ERR_SHAPE, "heads must be > 0");
+  if (!std::isfinite(position_divisor) || position_divisor <= 0.0f)
+    return set_err(SPISSA_ERR_INVALID_TENSOR_DATA,
+                   "gemma rotary position_divisor must be finite and positive, got %g", position_divisor);
+  const size_t eq = cfg->seq_len * q_heads * cfg->head_dim;
+  const size_t ek = cfg->seq_len * k_heads * cfg->head_dim;
+  if (q_len != eq || k_len != ek)
+    return set_err(SPISSA_ERR_SHAPE, "gemma rotary shape mismatch: q=%zu, expected=%zu, k=%zu, expected=%zu", q_len,
+                   eq, k_len, ek);
+  ST_TRY(guard_half(cfg));
+  if ((!q && q_len) || (!k && k_len)) return set_err(SPISSA_ERR_ARGUMENT, "q/k are null");
+  return rope_dropin(SPISSA_ROPE_GEMMA, q, q_len, k, k_len, q_heads, k_heads, cfg, position_divisor,
+                     nullptr, 0);
+  GUARD_END
+}
+
+extern "C" int spissa_rope_table_new(spissa_session *s, int kind, size_t rotary_dim, float base,
+                                     float position_divisor, const float *freq_scale,
+                                     size_t freq_scale_len, size_t max_positions,
+                                     spissa_rope_table **out) {
+  GUARD_BEGIN
+  if (!s || !out) return set_err(SPISSA_ERR_ARGUMENT, "null argument");
+  *out = nullptr;
+  if (kind != SPISSA_ROPE_LLAMA && kind != SPISSA_ROPE_GEMMA && kind != SPISSA_ROPE_NEOX)
+    return set_err(SPISSA_ERR_ARGUMENT, "unknown rope kind %d", kind);
+  if (rotary_dim < 2 || max_positions == 0)
+    return set_err(SPISSA_ERR_SHAPE, "rope table needs rotary_dim >= 2 and max_positions > 0");
+  if (kind == SPISSA_ROPE_NEOX && (rotary_dim % 2 != 0 || !std::isfinite(base) || base <= 0.0f))
+    return set_err(base <= 0.0f || !std::isfinite(base) ? SPISSA_ERR_INVALID_TENSOR_DATA : SPISSA_ERR_SHAPE,
+                   "invalid gpt-neox rotary parameters");
+  if (kind == SPISSA_ROPE_GEMMA && (!std::isfinite(position_divisor) || position_divisor <= 0.0f))
+    return set_err(SPISSA_ERR_INVALID_TENSOR_DATA,
+                   "gemma rotary position_divisor must be finite and positive, got %g", position_divisor);
+  const size_t half = rotary_dim / 2;
+  size_t n;
+  if (mul_ovf(max_positions, half, &n)) return set_err(SPISSA_ERR_SHAPE, "rope table size overflow");
+  std::vector<float> cs(n), sn(n);
+  fill_table(kind, rotary_dim, half, base, position_divisor, freq_scale, freq_scale ? freq_scale_len : 0, 0,
+             max_positions, cs.data(), sn.data());
+  std::unique_ptr<spissa_rope_table> t(new spissa_rope_table());
+  t->device = s->device;
+  t->kind = kind;
+  t->rotary_dim = rotary_dim;
+  t->half = half;
+  t->max_positions = max_positions;
+  HIP_TRY(hipSetDevice(s->device));
+  HIP_TRY(hipMalloc(&t->cos, n * sizeof(float)));
+  HIP_TRY(hipMalloc(&t->sin, n * sizeof(float)));
+  HIP_TRY(hipMemcpy(t->cos, cs.data(), n * sizeof(float), hipMemcpyHostToDevice));
+  HIP_TRY(hipMemcpy(t->sin, sn.data(), n * sizeof(float), hipMemcpyHostToDevice));
+  *out = t.release();
+  return SPISSA_OK;
+  GUARD_END
+}
+
+extern "C" void spissa_rope_table_free(spissa_rope_table *t) {
+  if (!t) return;
+  (void)hipSetDevice(t->device);
+  (void)hipDeviceSynchronize();
+  if (t->cos) (void)hipFree(t->cos);
+  if (t->sin) (void)hipFree(t->sin);
+  delete t;
+}
+
+static int table_check(const spissa_rope_table *t, size_t seq_len, size_t head_dim, size_t offset) {
+  if (2 * t->half > head_dim)
+    return set_err(SPISSA_ERR_SHAPE, "rotary_dim %zu exceeds head_dim %zu", t->rotary_dim, head_dim);
+  size_t end;
+  if (__builtin_add_overflow(offset, seq_len, &end) || end > t->max_positions)
+    return set_err(SPISSA_ERR_SHAPE, "positions %zu..%zu exceed the rope table (%zu positions)", offset,
+                   offset + seq_len, t->max_positions);
+  return SPISSA_OK;
+}
+
+extern "C" int spissa_rope_apply_device(spissa_session *s, const spissa_rope_table *t, float *d_q,
+                                        float *d_k, size_t seq_len, size_t q_heads, size_t k_heads,
+                                        size_t head_dim, size_t position_offset) {
+  GUARD_BEGIN
+  if (!s || !t) return set_err(SPISSA_ERR_ARGUMENT, "null argument");
+  if (q_heads == 0 || k_heads == 0) return set_err(SPISSA_ERR_SHAPE, "heads must be > 0");
+  ST_TRY(table_check(t, seq_len, head_dim, position_offset));
+  HIP_TRY(hipSetDevice(s->device));
+  HIP_TRY(launch_rope_apply(s->stream, t->cos + position_offset * t->half, t->sin + position_offset * t->half,
+                            t->half, d_q, d_k, seq_len, q_heads, k_heads, head_dim, t->half));
+  return SPISSA_OK;
+  GUARD_END
+}
+
+// ------------------------------------------------------------------------
+// RMSNorm and the Gemma prologue
+// ------------------------------------------------------------------------
+extern "C" int spissa_rms_norm(const float *x, size_t x_len, const float *weight, size_t weight_len,
+                               size_t rows, size_t cols, float eps, float *out, size_t out_len) {
+  GUARD_BEGIN
+  // ops.rs:160-166
+  if (x_len != rows * cols || weight_len != cols)
+    return set_err(SPISSA_ERR_SHAPE, "rms_norm shape mismatch: x=%zu, rows=%zu, cols=%zu, weight=%zu", x_len, rows,
+                   cols, weight_len);
+  if (out_len != x_len) return set_err(SPISSA_ERR_SHAPE, "rms_norm output holds %zu floats, need %zu", out_len, x_len);
+  if (x_len == 0) return SPISSA_OK;
+  if (!x || !weight || !out) return set_err(SPISSA_ERR_ARGUMENT, "null buffer");
+  spissa_session *s = nullptr;
+  ST_TRY(spissa_default_session(&s));
+  float *r[3];
+  ST_TRY(io_regions(s, {x_len, cols, x_len}, r));
+  HIP_TRY(hipSetDevice(s->device));
+  ST_TRY(h2d(s, r[0], x, x_len * sizeof(float)));
+  ST_TRY(h2d(s, r[1], weight, cols * sizeof(float)));
+  HIP_TRY(launch_rms_norm(s->stream, r[0], r[1], rows, cols, eps, r[2]));
+  ST_TRY(d2h(s, out, r[2], x_len * sizeof(float)));
+  return sync_stream(s);
+  GUARD_END
+}
+
+extern "C" int spissa_rms_norm_device(spissa_session *s, const float *d_x, const float *d_weight, size_t rows,
+                                      size_t cols, float eps, float *d_out) {
+  GUARD_BEGIN
+  if (!s) return set_err(SPISSA_ERR_ARGUMENT, "session is null");
+  HIP_TRY(hipSetDevice(s->device));
+  HIP_TRY(launch_rms_norm(s->stream, d_x, d_weight, rows, cols, eps, d_out));
+  return SPISSA_OK;
+  GUARD_END
+}
+
+extern "C" int spissa_is_global_layer(size_t layer_idx, size_t pattern) {
+  // models/gemma/model.rs:46-51
+  if (pattern <= 1) return 1;
+  return (layer_idx + 1) % pattern == 0;
+}
+
+extern "C" int spissa_gemma_qk_prologue_device(spissa_session *s, const spissa_rope_table *t, float *d_q,
+                                               float *d_k, size_t seq_len, size_t q_heads, size_t kv_heads,
+                                               size_t head_dim, const float *d_q_norm, const float *d_k_norm,
+                                               float eps, size_t position_offset, float q_prescale) {
+  GUARD_BEGIN
+  if (!s || !t) return set_err(SPISSA_ERR_ARGUMENT, "null argument");
+  if (t->kind != SPISSA_ROPE_GEMMA) return set_err(SPISSA_ERR_ARGUMENT, "the gemma prologue needs a gemma rope table");
+  if (q_heads == 0 || kv_heads == 0 || head_dim == 0) return set_err(SPISSA_ERR_SHAPE, "dimensions must be > 0");
+  ST_TRY(table_check(t, seq_len, head_dim, position_offset));
+  HIP_TRY(hipSetDevice(s->device));
+  HIP_TRY(launch_gemma_prologue(s->stream, t->cos + position_offset * t->half, t->sin + position_offset * t->half,
+                                t->half, d_q, d_k, seq_len, q_heads, kv_heads, head_dim, t->half, d_q_norm,
+                                d_k_norm, eps, q_prescale));
+  return SPISSA_OK;
+  GUARD_END
+}
+
+// ------------------------------------------------------------------------
+// Attention (rotary.rs:335-415)
+// ------------------------------------------------------------------------
+static int validate_attention(size_t q_len, size_t k_len, size_t v_len, const spissa_kv_cache *cache,
+                              const spissa_kv_attention_config *c, bool check_lens) {
+  // rotary.rs:483-547, same order.
+  if (c->query_len == 0 || c->num_heads == 0 || c->kv_heads == 0 || c->head_dim == 0)
+    return set_err(SPISSA_ERR_SHAPE,
+                   "KV attention dimensions must be non-zero, got query_len=%zu, num_heads=%zu, kv_heads=%zu, "
+                   "head_dim=%zu",
+                   c->query_len, c->num_heads, c->kv_heads, c->head_dim);
+  if (c->num_heads % c->kv_heads != 0)
+    return set_err(SPISSA_ERR_SHAPE, "query heads %zu must be a multiple of key/value heads %zu", c->num_heads,
+                   c->kv_heads);
+  size_t eq, ekv;
+  if (mul_ovf(c->query_len, c->num_heads, &eq) || mul_ovf(eq, c->head_dim, &eq))
+    return set_err(SPISSA_ERR_SHAPE, "KV attention current length overflow");
+  if (mul_ovf(c->query_len, c->kv_heads, &ekv) || mul_ovf(ekv, c->head_dim, &ekv))
+    return set_err(SPISSA_ERR_SHAPE, "KV attention current length overflow");
+  if (check_lens && (q_len != eq || k_len != ekv || v_len != ekv))
+    return set_err(SPISSA_ERR_SHAPE, "KV attention shape mismatch: expected q=%zu, k/v=%zu, got q=%zu, k=%zu, v=%zu",
+                   eq, ekv, q_len, k_len, v_len);
+  if (cache && (cache->num_heads != c->kv_heads || cache->head_dim != c->head_dim))
+    return set_err(SPISSA_ERR_SHAPE, "KV cache shape mismatch: cache heads/dim=%zu/%zu, attention kv_heads/dim=%zu/%zu",
+                   cache->num_heads, cache->head_dim, c->kv_heads, c->head_dim);
+  size_t past = cache ? cache->len : 0, key_len;
+  if (__builtin_add_overflow(past, c->query_len, &key_len)) return set_err(SPISSA_ERR_SHAPE, "KV attention key length overflow");
+  // Device index arithmetic is 32-bit in the key dimension.
+  if (key_len > (size_t)INT32_MAX / 2 || c->num_heads > 65535 || c->window > (size_t)INT32_MAX)
+    return set_err(SPISSA_ERR_SHAPE, "attention sizes exceed the device kernels' limits");
+  return SPISSA_OK;
+}
+
+static int pick_rb(int R) {
+  if (R % 4 == 0) return 4;
+  if (R % 3 == 0) return 3;
+  if (R % 2 == 0) return 2;
+  return 1;
+}
+
+static int run_decode(spissa_session *s, const float *d_q, const float *d_k, const float *d_v,
+                      const spissa_kv_cache *const *caches, size_t batch, const spissa_kv_attention_config *c,
+                      float *d_out) {
+  const int D = (int)c->head_dim, Hq = (int)c->num_heads, Hkv = (int)c->kv_heads;
+  const int R = Hq / Hkv;
+  const int RB = pick_rb(R);
+  const int HB = R / RB;
+  for (size_t b0 = 0; b0 < batch; b0 += kMaxDecodeBatch) {
+    const int B = (int)std::min<size_t>(kMaxDecodeBatch, batch - b0);
+    DecodeArgs a;
+    memset(&a, 0, sizeof a);
+    long total_rows = 0;
+    int max_keys = 0;
+    for (int b = 0; b < B; ++b) {
+      const spissa_kv_cache *cb = caches ? caches[b0 + b] : nullptr;
+      const int P = cb ? (int)cb->len : 0;
+      a.seq[b].k = cb ? cb->keys : nullptr;
+      a.seq[b].v = cb ? cb->values : nullptr;
+      a.seq[b].past = P;
+      int keys = P + 1;
+      if (c->window > 0) keys = std::min<int>(keys, (int)c->window);
+      max_keys = std::max(max_keys, keys);
+      total_rows += (long)keys * Hkv * HB;
+    }
+    const int kps = decode_keys_per_split(D, RB, total_rows, max_keys);
+    const int max_splits = (max_keys + kps - 1) / kps;
+    const int entries = combine_tree_entries(max_splits);
+    const int ctrs = std::max(1, combine_tree_counters(max_splits));
+    const size_t groups = (size_t)B * Hkv * HB;
+    ST_TRY(ensure_buf(s, s->partial, groups * entries * RB * (D + 2) * sizeof(float), false));
+    ST_TRY(ensure_buf(s, s->counters, groups * ctrs * sizeof(int), true));
+    a.q = d_q + b0 * (size_t)Hq * D;
+    a.cur_k = d_k + b0 * (size_t)Hkv * D;
+    a.cur_v = d_v + b0 * (size_t)Hkv * D;
+    a.out = d_out + b0 * (size_t)Hq * D;
+    a.partial = (float *)s->partial.p;
+    a.counters = (int *)s->counters.p;
+    a.err = s->d_err;
+    a.B = B;
+    a.Hq = Hq;
+    a.Hkv = Hkv;
+    a.R = R;
+    a.HB = HB;
+    a.window = (int)c->window;
+    a.kps = kps;
+    a.max_entries = entries;
+    a.max_counters = ctrs;
+    a.qscale = (1.0f / sqrtf((float)D)) * 1.4426950408889634f;
+    HIP_TRY(launch_decode(s->stream, a, D, RB, max_splits));
+  }
+  return SPISSA_OK;
+}
+
+static int run_generic(spissa_session *s, const float *d_q, const float *d_k, const float *d_v,
+                       const spissa_kv_cache *cache, const spissa_kv_attention_config *c, float *d_out) {
+  GenericArgs g;
+  g.q = d_q;
+  g.cur_k = d_k;
+  g.cur_v = d_v;
+  g.cache_k = cache ? cache->keys : nullptr;
+  g.cache_v = cache ? cache->values : nullptr;
+  g.out = d_out;
+  g.err = s->d_err;
+  g.S = (int)c->query_len;
+  g.P = cache ? (int)cache->len : 0;
+  g.Hq = (int)c->num_heads;
+  g.Hkv = (int)c->kv_heads;
+  g.D = (int)c->head_dim;
+  g.R = g.Hq / g.Hkv;
+  g.causal = c->causal ? 1 : 0;
+  g.window = (int)c->window;
+  g.scale = 1.0f / sqrtf((float)c->head_dim);
+  if (g.D > 1024) return set_err(SPISSA_ERR_SHAPE, "head_dim %d exceeds the f32 kernel's limit of 1024", g.D);
+  HIP_TRY(launch_generic(s->stream, g));
+  return SPISSA_OK;
+}
+
+static int run_prefill(spissa_session *s, const float *d_q, const float *d_k, const float *d_v,
+                       spissa_kv_cache *cache, const spissa_kv_attention_config *c, float *d_out) {
+  const int D = (int)c->head_dim, Hkv = (int)c->kv_heads;
+  const int P = cache ? (int)cache->len : 0;
+  const int S = (int)c->query_len;
+  const int P8 = P & ~7;
+  if (cache && P8 > 0) ST_TRY(ensure_shadow(cache, s->stream));
+  const size_t cap_stage = (((size_t)P + S + 63) & ~(size_t)63) - P8;
+  ST_TRY(ensure_buf(s, s->stage, 2 * (size_t)Hkv * cap_stage * D * sizeof(bf16), false));
+  bf16 *kb_stage = (bf16 *)s->stage.p;
+  bf16 *vt_stage = kb_stage + (size_t)Hkv * cap_stage * D;
+  const size_t w = (size_t)Hkv * D;
+  const int tail = P - P8;  // cached rows re-staged so the staging buffer starts 8-aligned
+  if (tail > 0)
+    HIP_TRY(launch_stage_bf16(s->stream, cache->keys + (size_t)P8 * w, cache->values + (size_t)P8 * w, tail, tail,
+                              Hkv, D, kb_stage, vt_stage, 0, cap_stage));
+  HIP_TRY(launch_stage_bf16(s->stream, d_k, d_v, S, cap_stage - tail, Hkv, D, kb_stage, vt_stage, tail, cap_stage));
+  PrefillArgs a;
+  memset(&a, 0, sizeof a);
+  a.q = d_q;
+  a.out = d_out;
+  a.kb_cache = cache ? cache->kb : nullptr;
+  a.vt_cache = cache ? cache->vt : nullptr;
+  a.kb_stage = kb_stage;
+  a.vt_stage = vt_stage;
+  a.cap_cache = cache ? (long)cache->shadow_cap : 0;
+  a.cap_stage = (long)cap_stage;
+  a.P = P;
+  a.P8 = P8;
+  a.S = S;
+  a.Hq = (int)c->num_heads;
+  a.Hkv = Hkv;
+  a.R = a.Hq / Hkv;
+  a.causal = c->causal ? 1 : 0;
+  a.window = (int)c->window;
+  a.err = s->d_err;
+  a.qk_scale_log2 = (1.0f / sqrtf((float)D)) * 1.4426950408889634f;
+  HIP_TRY(launch_prefill(s->stream, a, D));
+  return SPISSA_OK;
+}
+
+static int attention_device_impl(spissa_session *s, const float *d_q, const float *d_k, const float *d_v,
+                                 const spissa_kv_cache *cache, const spissa_kv_attention_config *c, float *d_out) {
+  HIP_TRY(hipSetDevice(s->device));
+  const int D = (int)c->head_dim;
+  const int R = (int)(c->num_heads / c->kv_heads);
+  if (c->query_len == 1 && decode_supported(D, R)) return run_decode(s, d_q, d_k, d_v, &cache, 1, c, d_out);
+  if (c->query_len > 1 && s->prefill_precision == SPISSA_PREFILL_BF16 && prefill_supported(D))
+    return run_prefill(s, d_q, d_k, d_v, const_cast<spissa_kv_cache *>(cache), c, d_out);
+  return run_generic(s, d_q, d_k, d_v, cache, c, d_out);
+}
+
+extern "C" int spissa_attention_device(spissa_session *s, const float *d_q, const float *d_k, const float *d_v,
+                                       const spissa_kv_cache *cache, const spissa_kv_attention_config *cfg,
+                                       float *d_out) {
+  GUARD_BEGIN
+  if (!s || !cfg) return set_err(SPISSA_ERR_ARGUMENT, "null argument");
+  ST_TRY(validate_attention(0, 0, 0, cache, cfg, false));
+  if (cache && cache->session->device != s->device)
+    return set_err(SPISSA_ERR_ARGUMENT, "cache lives on device %d, session on %d", cache->session->device, s->device);
+  return attention_device_impl(s, d_q, d_k, d_v, cache, cfg, d_out);
+  GUARD_END
+}
+
+extern "C" int spissa_attention_decode_batch_device(spissa_session *s, const float *d_q, const float *d_k,
+                                                    const float *d_v, const spissa_kv_cache *const *caches,
+                                                    size_t batch, const spissa_kv_attention_config *cfg,
+                                                    float *d_out) {
+  GUARD_BEGIN
+  if (!s || !cfg) return set_err(SPISSA_ERR_ARGUMENT, "null argument");
+  if (cfg->query_len != 1) return set_err(SPISSA_ERR_SHAPE, "batched decode needs query_len == 1, got %zu", cfg->query_len);
+  for (size_t b = 0; b < batch; ++b) ST_TRY(validate_attention(0, 0, 0, caches ? caches[b] : nullptr, cfg, false));
+  if (batch == 0) return SPISSA_OK;
+  HIP_TRY(hipSetDevice(s->device));
+  const int D = (int)cfg->head_dim;
+  const int R = (int)(cfg->num_heads / cfg->kv_heads);
+  if (decode_supported(D, R)) return run_decode(s, d_q, d_k, d_v, caches, batch, cfg, d_out);
+  for (size_t b = 0; b < batch; ++b) {
+    const size_t qo = b * cfg->num_heads * cfg->head_dim, ko = b * cfg->kv_heads * cfg->head_dim;
+    ST_TRY(run_generic(s, d_q + qo, d_k + ko, d_v + ko, caches ? caches[b] : nullptr, cfg, d_out + qo));
+  }
+  return SPISSA_OK;
+  GUARD_END
+}
+
+extern "C" int spissa_scaled_dot_product_attention_with_cache(const float *q, size_t q_len, const float *current_k,
+                                                              size_t k_len, const float *current_v, size_t v_len,
+                                                              const spissa_kv_cache *cache,
+                                                              const spissa_kv_attention_config *cfg, float *out,
+                                                              size_t out_len) {
+  GUARD_BEGIN
+  if (!cfg) return set_err(SPISSA_ERR_ARGUMENT, "config is null");
+  ST_TRY(validate_attention(q_len, k_len, v_len, cache, cfg, true));
+  if (out_len != q_len) return set_err(SPISSA_ERR_SHAPE, "output holds %zu floats, need %zu", out_len, q_len);
+  if (!q || !current_k || !current_v || !out) return set_err(SPISSA_ERR_ARGUMENT, "null buffer");
+  spissa_session *s = nullptr;
+  ST_TRY(spissa_default_session(&s));
+  if (cache && cache->session->device != s->device)
+    return set_err(SPISSA_ERR_ARGUMENT, "cache lives on device %d, the calling thread on %d", cache->session->device,
+                   s->device);
+  if (cache && cache->session != s) HIP_TRY(hipStreamSynchronize(cache->session->stream));
+  float *r[4];
+  ST_TRY(io_regions(s, {q_len, k_len, v_len, q_len}, r));
+  HIP_TRY(hipSetDevice(s->device));
+  ST_TRY(h2d(s, r[0], q, q_len * sizeof(float)));
+  ST_TRY(h2d(s, r[1], current_k, k_len * sizeof(float)));
+  ST_TRY(h2d(s, r[2], current_v, v_len * sizeof(float)));
+  ST_TRY(attention_device_impl(s, r[0], r[1], r[2], cache, cfg, r[3]));
+  ST_TRY(spissa_session_sync(s));
+  ST_TRY(d2h(s, out, r[3], q_len * sizeof(float)));
+  return sync_stream(s);
+  GUARD_END
+}
+
+extern "C" int spissa_scaled_dot_product_attention(const float *q, size_t q_len, const float *k, size_t k_len,
+                                                   const float *v, size_t v_len, size_t seq_len, size_t num_heads,
+                                                   size_t head_dim, int causal, float *out, size_t out_len) {
+  GUARD_BEGIN
+  // ops.rs:246-255
+  const size_t expected = seq_len * num_heads * head_dim;
+  if (q_len != expected || k_len != expected || v_len != expected)
+    return set_err(SPISSA_ERR_SHAPE, "attention shape mismatch: expected %zu, got q=%zu, k=%zu, v=%zu", expected,
+                   q_len, k_len, v_len);
+  if (out_len != expected) return set_err(SPISSA_ERR_SHAPE, "output holds %zu floats, need %zu", out_len, expected);
+  if (expected == 0) return SPISSA_OK;
+  spissa_kv_attention_config c = {seq_len, num_heads, num_heads, head_dim, causal, 0};
+  return spissa_scaled_dot_product_attention_with_cache(q, q_len, k, k_len, v, v_len, nullptr, &c, out, out_len);
+  GUARD_END
+}

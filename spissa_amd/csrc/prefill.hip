@@ -1,0 +1,264 @@
+// prefill.hip -- causal GQA prefill (rotary.rs:335-415 with query_len > 1,
+// including chunked prefill against a cache and the sliding-window extension)
+// as a bf16-MFMA flash-attention kernel for gfx950. Inputs and outputs are
+// f32; Q is rounded to bf16 in registers, K and V are read from bf16 copies
+// (the cache's bf16 shadow for keys already cached, a staging buffer for the
+// rest); scores, softmax state and the output accumulate in f32.
+//
+// Tiling. A workgroup owns NPB blocks of 32 query positions for RB query
+// heads of one KV head (NW = RB*NPB waves, one 32-query block of one head per
+// wave), so every K/V tile staged in LDS serves all RB heads of the group.
+// Per key tile of BN keys a wave computes
+//   S^T = K Q^T   with v_mfma_f32_32x32x16_bf16 (A = K rows from LDS, B = Q in
+//                 registers); the accumulator layout puts one query per lane
+//                 (lane & 31) and 16 of its keys per lane, so the row max and
+//                 sum are lane-local plus one v_permlane32_swap;
+//   O^T += V^T P^T with the same instruction (A = V^T from the transposed LDS
+//                 tile, B = P^T straight from the score registers: the key
+//                 order of the contraction is permuted consistently on both
+//                 operands, so no register shuffle is needed).
+// The online softmax runs in the log2 domain with v_exp_f32.
+// Workgroups are issued longest (last query tile) first for causal balance.
+#include "internal.hpp"
+
+namespace spissa {
+
+namespace {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float xor32_max(float v) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ bf16x8 cat(bf16x4 a, bf16x4 b) {
+  return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+}  // namespace
+
+template <int D, int RB, int NPB, int BN>
+__global__ __launch_bounds__(RB *NPB * 64) void prefill_kernel(const PrefillArgs a) {
+  constexpr int NW = RB * NPB;
+  constexpr int NT = NW * 64;
+  constexpr int KS = D + 8;   // K tile row stride (bf16), padded against LDS bank conflicts
+  constexpr int VS = BN + 4;  // V^T tile row stride (bf16)
+  constexpr int WGQ = NPB * 32;
+  constexpr int DB = D / 32;  // 32-dim output blocks
+  constexpr int KB = BN / 32; // 32-key score blocks
+  constexpr float NEG_INF = -__builtin_inff();
+
+  __shared__ __attribute__((aligned(16))) bf16 Ks[BN * KS];
+  __shared__ __attribute__((aligned(16))) bf16 Vs[D * VS];
+
+  const int HB = a.R / RB;
+  int bid = blockIdx.x;
+  const int hh = bid % (a.Hkv * HB);
+  bid /= (a.Hkv * HB);
+  const int qt = a.n_qblocks - 1 - bid;  // longest rows first
+  const int h = hh / HB, hb = hh % HB;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int r = wave % RB, pb = wave / RB;
+  const int head = h * a.R + hb * RB + r;
+  const int p0 = qt * WGQ;
+  const int wp0 = p0 + pb * 32;
+  const int lq = lane & 31, hl = lane >> 5;
+  const int my_pos = wp0 + lq;
+  const bool pos_ok = my_pos < a.S;
+  const int q_abs = a.P + my_pos;
+  const int key_total = a.P + a.S;
+
+  int key_end = key_total;
+  if (a.causal) key_end = min(key_total, a.P + min(a.S, p0 + WGQ));
+  int key_begin = 0;
+  if (a.window > 0) key_begin = max(0, a.P + p0 - a.window + 1);
+  const int t_begin = key_begin / BN;
+  const int t_end = (key_end + BN - 1) / BN;
+
+  // Q as the B operand of S^T = K Q^T: lane holds query lq, dims 16t + 8hl + [0,8).
+  bf16x8 qf[D / 16];
+  {
+    const int pos = min(my_pos, a.S - 1);
+    const float *qp = a.q + ((long)pos * a.Hq + head) * D + 8 * hl;
+#pragma unroll
+    for (int t = 0; t < D / 16; ++t) {
+      const float4 x0 = *reinterpret_cast<const float4 *>(qp + 16 * t);
+      const float4 x1 = *reinterpret_cast<const float4 *>(qp + 16 * t + 4);
+      bf16x8 v;
+      v[0] = (bf16)x0.x; v[1] = (bf16)x0.y; v[2] = (bf16)x0.z; v[3] = (bf16)x0.w;
+      v[4] = (bf16)x1.x; v[5] = (bf16)x1.y; v[6] = (bf16)x1.z; v[7] = (bf16)x1.w;
+      qf[t] = v;
+    }
+  }
+
+  f32x16 oacc[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) oacc[d][i] = 0.0f;
+  float m = NEG_INF, l = 0.0f;
+
+  const int wave_min_q = a.P + wp0;
+  const int wave_max_q = a.P + min(wp0 + 31, a.S - 1);
+  const bool wave_live = wp0 < a.S;
+
+  for (int t = t_begin; t < t_end; ++t) {
+    const int kt0 = t * BN;
+    __syncthreads();
+    // ---- stage the K tile [BN][D] and the V^T tile [D][BN] in LDS ----
+    for (int c = threadIdx.x; c < BN * (D / 8); c += NT) {
+      const int row = c / (D / 8), col = (c % (D / 8)) * 8;
+      const int key = kt0 + row;
+      const bf16 *src = key < a.P8
+                            ? a.kb_cache + ((long)h * a.cap_cache + key) * D
+                            : a.kb_stage + ((long)h * a.cap_stage + (key - a.P8)) * D;
+      *reinterpret_cast<uint4 *>(&Ks[row * KS + col]) = *reinterpret_cast<const uint4 *>(src + col);
+    }
+    for (int c = threadIdx.x; c < D * (BN / 8); c += NT) {
+      const int dim = c / (BN / 8), kc = (c % (BN / 8)) * 8;
+      const int key = kt0 + kc;
+      const bf16 *src = key < a.P8
+                            ? a.vt_cache + ((long)h * D + dim) * a.cap_cache + key
+                            : a.vt_stage + ((long)h * D + dim) * a.cap_stage + (key - a.P8);
+      const uint4 v = *reinterpret_cast<const uint4 *>(src);
+      *reinterpret_cast<uint2 *>(&Vs[dim * VS + kc]) = make_uint2(v.x, v.y);
+      *reinterpret_cast<uint2 *>(&Vs[dim * VS + kc + 4]) = make_uint2(v.z, v.w);
+    }
+    __syncthreads();
+
+    const bool active = wave_live && !(a.causal && kt0 > wave_max_q) &&
+                        !(a.window > 0 && kt0 + BN - 1 + a.window <= wave_min_q);
+    if (!active) continue;
+
+    // ---- S^T = K Q^T ----
+    f32x16 sacc[KB];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sacc[kb][i] = 0.0f;
+#pragma unroll
+      for (int tt = 0; tt < D / 16; ++tt) {
+        const bf16x8 ka =
+            *reinterpret_cast<const bf16x8 *>(&Ks[(kb * 32 + lq) * KS + 16 * tt + 8 * hl]);
+        sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[tt], sacc[kb], 0, 0, 0);
+      }
+    }
+
+    // ---- mask, scale, online softmax ----
+    const bool need_mask = (a.causal && kt0 + BN - 1 > wave_min_q) ||
+                           (a.window > 0 && kt0 + a.window <= wave_max_q) ||
+                           (kt0 + BN > key_total);
+    float tmax = NEG_INF;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        float s = sacc[kb][i] * a.qk_scale_log2;
+        if (need_mask) {
+          const int key = kt0 + kb * 32 + 8 * (i >> 2) + 4 * hl + (i & 3);
+          const bool masked = (a.causal && key > q_abs) ||
+                              (a.window > 0 && key + a.window <= q_abs) || key >= key_total;
+          if (masked) s = NEG_INF;
+        }
+        sacc[kb][i] = s;
+        tmax = fmaxf(tmax, s);
+      }
+    }
+    tmax = xor32_max(tmax);
+    const float mnew = fmaxf(m, tmax);
+    const float ms = mnew == NEG_INF ? 0.0f : mnew;
+    const float alpha = fast_exp2(m - ms);
+    m = mnew;
+    l *= alpha;
+#pragma unroll
+    for (int d = 0; d < DB; ++d)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) oacc[d][i] *= alpha;
+
+    // ---- O^T += V^T P^T ----
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      bf16x8 pa, pb;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float p0v = fast_exp2(sacc[kb][i] - ms);
+        const float p1v = fast_exp2(sacc[kb][i + 8] - ms);
+        l += p0v + p1v;
+        pa[i] = (bf16)p0v;
+        pb[i] = (bf16)p1v;
+      }
+#pragma unroll
+      for (int d = 0; d < DB; ++d) {
+        const bf16 *vrow = &Vs[(d * 32 + lq) * VS + kb * 32 + 4 * hl];
+        const bf16x8 va = cat(*reinterpret_cast<const bf16x4 *>(vrow),
+                              *reinterpret_cast<const bf16x4 *>(vrow + 8));
+        oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pa, oacc[d], 0, 0, 0);
+        const bf16x8 vb = cat(*reinterpret_cast<const bf16x4 *>(vrow + 16),
+                              *reinterpret_cast<const bf16x4 *>(vrow + 24));
+        oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vb, pb, oacc[d], 0, 0, 0);
+      }
+    }
+  }
+
+  // ---- epilogue: O = O^T / l ----
+  const float lt = xor32_sum(l);
+  if (pos_ok) {
+    if (hl == 0 && !(lt > 0.0f && lt < __builtin_inff())) atomicOr(a.err, kDevErrSoftmaxDenominator);
+    const float inv = 1.0f / lt;
+    float *op = a.out + ((long)my_pos * a.Hq + head) * D + 4 * hl;
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        float4 v = make_float4(oacc[d][4 * g] * inv, oacc[d][4 * g + 1] * inv,
+                               oacc[d][4 * g + 2] * inv, oacc[d][4 * g + 3] * inv);
+        *reinterpret_cast<float4 *>(op + d * 32 + 8 * g) = v;
+      }
+    }
+  }
+}
+
+namespace {
+
+template <int D, int RB, int NPB>
+hipError_t launch_cfg(hipStream_t st, PrefillArgs a) {
+  constexpr int BN = D >= 256 ? 32 : 64;
+  constexpr int WGQ = NPB * 32;
+  a.n_qblocks = (a.S + WGQ - 1) / WGQ;
+  const long blocks = (long)a.n_qblocks * a.Hkv * (a.R / RB);
+  hipLaunchKernelGGL((prefill_kernel<D, RB, NPB, BN>), dim3((unsigned)blocks), dim3(RB * NPB * 64),
+                     0, st, a);
+  return hipGetLastError();
+}
+
+template <int D>
+hipError_t launch_d(hipStream_t st, const PrefillArgs &a) {
+  if (a.R % 4 == 0) return launch_cfg<D, 4, 1>(st, a);
+  if (a.R % 3 == 0) return launch_cfg<D, 3, 1>(st, a);
+  if (a.R % 2 == 0) return launch_cfg<D, 2, 2>(st, a);
+  return launch_cfg<D, 1, 4>(st, a);
+}
+
+}  // namespace
+
+bool prefill_supported(int D) { return D == 64 || D == 128 || D == 256; }
+
+hipError_t launch_prefill(hipStream_t st, const PrefillArgs &a, int D) {
+  switch (D) {
+    case 64: return launch_d<64>(st, a);
+    case 128: return launch_d<128>(st, a);
+    case 256: return launch_d<256>(st, a);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace spissa

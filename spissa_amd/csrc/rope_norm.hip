@@ -1,0 +1,171 @@
+// rope_norm.hip -- RoPE application, RMSNorm (Gemma QK-norm), the fused Gemma
+// Q/K prologue, and the f32 -> bf16 K / transposed-V staging used by prefill.
+//
+// RoPE and RMSNorm here are bit-identical to the Rust reference: cos/sin come
+// from a table computed on the host with the reference's own per-(position,
+// pair) formula and glibc libm, every multiply and add is rounded separately
+// (contraction off), and hipcc's default f32 division and sqrt are correctly
+// rounded.
+#include "internal.hpp"
+
+namespace spissa {
+
+// rotary.rs:467-481 rotate_neox_pair, applied to every (row, pair) in parallel.
+// Rows are S * (qh + kh): for each position, qh query rows then kh key rows.
+__global__ void rope_apply_kernel(const float *__restrict__ cos_tab,
+                                  const float *__restrict__ sin_tab, long tab_stride,
+                                  float *__restrict__ q, float *__restrict__ k, long S, int qh,
+                                  int kh, int D, int half) {
+#pragma clang fp contract(off)
+  long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  long rows = S * (qh + kh);
+  if (t >= rows * half) return;
+  long row = t / half;
+  int pair = (int)(t - row * half);
+  long pos = row / (qh + kh);
+  int hh = (int)(row - pos * (qh + kh));
+  float *base = hh < qh ? q + (pos * qh + hh) * (long)D : k + (pos * kh + (hh - qh)) * (long)D;
+  float c = cos_tab[pos * tab_stride + pair];
+  float s = sin_tab[pos * tab_stride + pair];
+  float first = base[pair];
+  float second = base[pair + half];
+  base[pair] = first * c - second * s;
+  base[pair + half] = second * c + first * s;
+}
+
+// ops.rs:159-179 rms_norm: one thread per row, sequential sum of squares.
+__global__ void rms_norm_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                long rows, int cols, float eps, float *__restrict__ out) {
+#pragma clang fp contract(off)
+  long r = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const float *row = x + r * cols;
+  float acc = 0.0f;
+  for (int c = 0; c < cols; ++c) acc += row[c] * row[c];
+  float mean_square = acc / (float)cols;
+  float inv_rms = 1.0f / sqrtf(mean_square + eps);
+  float *o = out + r * cols;
+  for (int c = 0; c < cols; ++c) o[c] = row[c] * inv_rms * w[c];
+}
+
+// models/gemma/generate.rs:230-278 for one row of q or k: rms_norm, Gemma
+// rotate-half with the layer's table, then (q rows only) the prescale.
+__global__ void gemma_prologue_kernel(const float *__restrict__ cos_tab,
+                                      const float *__restrict__ sin_tab, long tab_stride,
+                                      float *__restrict__ q, float *__restrict__ k, long S, int qh,
+                                      int kh, int D, int half, const float *__restrict__ qn,
+                                      const float *__restrict__ kn, float eps, float prescale) {
+#pragma clang fp contract(off)
+  long row = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (row >= S * (qh + kh)) return;
+  long pos = row / (qh + kh);
+  int hh = (int)(row - pos * (qh + kh));
+  bool is_q = hh < qh;
+  float *x = is_q ? q + (pos * qh + hh) * (long)D : k + (pos * kh + (hh - qh)) * (long)D;
+  const float *w = is_q ? qn : kn;
+  float acc = 0.0f;
+  for (int c = 0; c < D; ++c) acc += x[c] * x[c];
+  float mean_square = acc / (float)D;
+  float inv_rms = 1.0f / sqrtf(mean_square + eps);
+  const float *ct = cos_tab + pos * tab_stride;
+  const float *st = sin_tab + pos * tab_stride;
+  for (int p = 0; p < half; ++p) {
+    float first = x[p] * inv_rms * w[p];
+    float second = x[p + half] * inv_rms * w[p + half];
+    float c = ct[p], s = st[p];
+    float a = first * c - second * s;
+    float b = second * c + first * s;
+    if (is_q) {
+      a *= prescale;
+      b *= prescale;
+    }
+    x[p] = a;
+    x[p + half] = b;
+  }
+  for (int c = 2 * half; c < D; ++c) {
+    float v = x[c] * inv_rms * w[c];
+    if (is_q) v *= prescale;
+    x[c] = v;
+  }
+}
+
+// Converts n rows of K and V ([n, H, D] f32) to the prefill operand layouts:
+// kb [H, cap, D] bf16 (head-major K) and vt [H, D, cap] bf16 (transposed V),
+// at buffer positions dst_first + i. Rows with i >= n (up to the tile's end)
+// are written as zeros so padded key tiles read finite data.
+// Grid: (ceil(n_pad/64), H, ceil(D/64)), 256 threads.
+__global__ void stage_bf16_kernel(const float *__restrict__ k_rows,
+                                  const float *__restrict__ v_rows, long n, long n_pad, int H,
+                                  int D, bf16 *__restrict__ kb, bf16 *__restrict__ vt,
+                                  long dst_first, long cap) {
+  __shared__ float tile[64][65];
+  const int h = blockIdx.y;
+  const long i0 = (long)blockIdx.x * 64;
+  const int d0 = blockIdx.z * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;  // 64 x 4
+  for (int ii = ty; ii < 64; ii += 4) {
+    long i = i0 + ii;
+    int d = d0 + tx;
+    if (i < n_pad && d < D) {
+      float kv = 0.0f, vv = 0.0f;
+      if (i < n) {
+        kv = k_rows[(i * H + h) * (long)D + d];
+        vv = v_rows[(i * H + h) * (long)D + d];
+      }
+      kb[((long)h * cap + dst_first + i) * D + d] = (bf16)kv;
+      tile[ii][tx] = vv;
+    }
+  }
+  __syncthreads();
+  for (int dd = ty; dd < 64; dd += 4) {
+    int d = d0 + dd;
+    long i = i0 + tx;
+    if (d < D && i < n_pad) vt[((long)h * D + d) * cap + dst_first + i] = (bf16)tile[tx][dd];
+  }
+}
+
+static inline unsigned blocks_for(long n, int per) { return (unsigned)((n + per - 1) / per); }
+
+hipError_t launch_rope_apply(hipStream_t st, const float *cos_tab, const float *sin_tab,
+                             size_t tab_stride, float *q, float *k, size_t S, size_t qh,
+                             size_t kh, size_t D, size_t half) {
+  long total = (long)S * (long)(qh + kh) * (long)half;
+  if (total == 0) return hipSuccess;
+  hipLaunchKernelGGL(rope_apply_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, st, cos_tab,
+                     sin_tab, (long)tab_stride, q, k, (long)S, (int)qh, (int)kh, (int)D, (int)half);
+  return hipGetLastError();
+}
+
+hipError_t launch_rms_norm(hipStream_t st, const float *x, const float *w, size_t rows,
+                           size_t cols, float eps, float *out) {
+  if (rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(rms_norm_kernel, dim3(blocks_for((long)rows, 64)), dim3(64), 0, st, x, w,
+                     (long)rows, (int)cols, eps, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemma_prologue(hipStream_t st, const float *cos_tab, const float *sin_tab,
+                                 size_t tab_stride, float *q, float *k, size_t S, size_t qh,
+                                 size_t kh, size_t D, size_t half, const float *qn,
+                                 const float *kn, float eps, float prescale) {
+  long rows = (long)S * (long)(qh + kh);
+  if (rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(gemma_prologue_kernel, dim3(blocks_for(rows, 64)), dim3(64), 0, st, cos_tab,
+                     sin_tab, (long)tab_stride, q, k, (long)S, (int)qh, (int)kh, (int)D, (int)half,
+                     qn, kn, eps, prescale);
+  return hipGetLastError();
+}
+
+hipError_t launch_stage_bf16(hipStream_t st, const float *k_rows, const float *v_rows, size_t n,
+                             size_t n_pad_rows, size_t H, size_t D, bf16 *kb, bf16 *vt,
+                             size_t dst_first, size_t dst_cap) {
+  long n_pad = (long)n_pad_rows;
+  if (n_pad <= 0) return hipSuccess;
+  if ((long)dst_first + n_pad > (long)dst_cap || n_pad < (long)n) return hipErrorInvalidValue;
+  dim3 grid(blocks_for(n_pad, 64), (unsigned)H, blocks_for((long)D, 64));
+  hipLaunchKernelGGL(stage_bf16_kernel, grid, dim3(256), 0, st, k_rows, v_rows, (long)n, n_pad,
+                     (int)H, (int)D, kb, vt, (long)dst_first, (long)dst_cap);
+  return hipGetLastError();
+}
+
+}  // namespace spissa

@@ -1,0 +1,152 @@
+"""Device fast path: sessions and `_device` entry points on HBM-resident buffers.
+
+Buffers are torch tensors on a ROCm device (float32, contiguous); torch only
+supplies device memory and streams here. Calls are asynchronous on the
+session's stream; `Session.sync()` waits and reports device-side errors
+(an invalid softmax denominator raises InvalidTensorDataError, as
+rotary.rs:560-564 does).
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import Optional, Sequence
+
+from . import _ffi
+from .errors import ArgumentError, check
+from .rotary import KvAttentionConfig, KvCache
+
+
+def _dev(t, name: str) -> int:
+    if t is None:
+        return 0
+    if not getattr(t, "is_cuda", False):
+        raise TypeError(f"{name} must be a device tensor")
+    import torch
+
+    if t.dtype != torch.float32 or not t.is_contiguous():
+        raise TypeError(f"{name} must be a contiguous float32 tensor")
+    return t.data_ptr()
+
+
+class RopeTable:
+    """A resident cos/sin table (spissa_rope_table_new)."""
+
+    def __init__(self, session: "Session", kind: int, rotary_dim: int, base: float,
+                 position_divisor: float = 1.0, freq_scale=None, max_positions: int = 8192):
+        import numpy as np
+
+        lib = _ffi.load()
+        self._lib = lib
+        fs = None
+        if freq_scale is not None:
+            fs = np.ascontiguousarray(np.asarray(freq_scale, dtype=np.float32))
+        h = _ffi.c_void_p()
+        check(lib.spissa_rope_table_new(
+            session.handle, kind, rotary_dim, base, position_divisor,
+            None if fs is None else fs.ctypes.data_as(_ffi.c_float_p), 0 if fs is None else fs.size,
+            max_positions, C.byref(h)))
+        self._h = h
+        self.kind = kind
+        self.rotary_dim = rotary_dim
+        self.max_positions = max_positions
+
+    @property
+    def handle(self):
+        return self._h
+
+    def close(self):
+        if getattr(self, "_h", None) is not None and self._h.value:
+            self._lib.spissa_rope_table_free(self._h)
+        self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Session:
+    """One device, one HIP stream (own or borrowed), one workspace."""
+
+    def __init__(self, device: int = 0, stream=None):
+        lib = _ffi.load()
+        self._lib = lib
+        handle = None
+        if stream is not None:
+            handle = stream if isinstance(stream, int) else stream.cuda_stream
+        h = _ffi.c_void_p()
+        check(lib.spissa_session_create(device, handle, C.byref(h)))
+        self._h = h
+        self.device = device
+
+    @property
+    def handle(self):
+        if self._h is None or not self._h.value:
+            raise ArgumentError("session has been closed")
+        return self._h
+
+    @property
+    def stream_handle(self) -> int:
+        return self._lib.spissa_session_stream(self.handle)
+
+    def close(self):
+        if getattr(self, "_h", None) is not None and self._h.value:
+            self._lib.spissa_session_destroy(self._h)
+        self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def sync(self) -> None:
+        check(self._lib.spissa_session_sync(self.handle))
+
+    def set_prefill_precision(self, precision: int) -> None:
+        check(self._lib.spissa_session_set_prefill_precision(self.handle, precision))
+
+    def kv_cache(self, num_heads: int, head_dim: int, max_seq_len: int) -> KvCache:
+        return KvCache(num_heads, head_dim, max_seq_len, session=self)
+
+    def rope_table(self, kind: int, rotary_dim: int, base: float, position_divisor: float = 1.0,
+                   freq_scale=None, max_positions: int = 8192) -> RopeTable:
+        return RopeTable(self, kind, rotary_dim, base, position_divisor, freq_scale, max_positions)
+
+    def rope_apply(self, table: RopeTable, q, k, seq_len: int, q_heads: int, k_heads: int,
+                   head_dim: int, position_offset: int) -> None:
+        check(self._lib.spissa_rope_apply_device(self.handle, table.handle, _dev(q, "q"),
+                                                 _dev(k, "k"), seq_len, q_heads, k_heads, head_dim,
+                                                 position_offset))
+
+    def rms_norm(self, x, weight, rows: int, cols: int, eps: float, out) -> None:
+        check(self._lib.spissa_rms_norm_device(self.handle, _dev(x, "x"), _dev(weight, "weight"),
+                                               rows, cols, eps, _dev(out, "out")))
+
+    def gemma_qk_prologue(self, table: RopeTable, q, k, seq_len: int, q_heads: int, kv_heads: int,
+                          head_dim: int, q_norm, k_norm, eps: float, position_offset: int,
+                          q_prescale: float) -> None:
+        check(self._lib.spissa_gemma_qk_prologue_device(
+            self.handle, table.handle, _dev(q, "q"), _dev(k, "k"), seq_len, q_heads, kv_heads,
+            head_dim, _dev(q_norm, "q_norm"), _dev(k_norm, "k_norm"), eps, position_offset,
+            q_prescale))
+
+    def attention(self, q, k, v, cache: Optional[KvCache], config: KvAttentionConfig, out) -> None:
+        cfg = config._c()
+        check(self._lib.spissa_attention_device(
+            self.handle, _dev(q, "q"), _dev(k, "k"), _dev(v, "v"),
+            None if cache is None else cache.handle, C.byref(cfg), _dev(out, "out")))
+
+    def attention_decode_batch(self, q, k, v, caches: Sequence[Optional[KvCache]],
+                               config: KvAttentionConfig, out) -> None:
+        arr = (_ffi.c_void_p * max(1, len(caches)))()
+        for i, c in enumerate(caches):
+            arr[i] = None if c is None else c.handle.value
+        cfg = config._c()
+        check(self._lib.spissa_attention_decode_batch_device(
+            self.handle, _dev(q, "q"), _dev(k, "k"), _dev(v, "v"), arr, len(caches), C.byref(cfg),
+            _dev(out, "out")))
+
+    def append(self, cache: KvCache, k, v, token_count: int) -> None:
+        cache.append_device(_dev(k, "k"), _dev(v, "v"), token_count)

@@ -1,0 +1,177 @@
+"""GPU parity of cached attention against the CPU oracle on identical seeded inputs.
+
+Tolerances (metric: max|gpu - ref| / max|ref| over the output tensor):
+  f32 decode (query_len == 1)         <= 1e-4
+  f32 prefill precision (SIMT kernel) <= 1e-4
+  bf16-MFMA prefill                   <= 1e-2
+Shapes are the BASELINE configs' head geometry at contexts the oracle finishes
+in seconds; full contexts are checked in test_gpu_scale.py.
+"""
+import numpy as np
+import pytest
+
+import oracle as o
+from tests.helpers import layer_inputs, rel_err
+
+pytestmark = pytest.mark.gpu
+
+DECODE_TOL = 1e-4
+F32_TOL = 1e-4
+BF16_TOL = 1e-2
+
+
+def run_both(gpu, config, layer, S, P, Hq, Hkv, D, window=0, causal=True, cap_extra=1):
+    q, k, v, pk, pv = layer_inputs(config, layer, S, P, Hq, Hkv, D)
+    cap = P + S + cap_extra
+    ref_cache = o.KvCache(Hkv, D, cap)
+    dev_cache = gpu.KvCache(Hkv, D, cap)
+    if P:
+        ref_cache.append(pk, pv, P)
+        dev_cache.append(pk, pv, P)
+    ref = o.sdpa_with_cache(q, k, v, ref_cache, S, Hq, Hkv, D, causal, window)
+    cfg = gpu.KvAttentionConfig(S, Hq, Hkv, D, causal, window)
+    got = gpu.scaled_dot_product_attention_with_cache(q, k, v, dev_cache, cfg)
+    return got, ref, dev_cache, (q, k, v)
+
+
+@pytest.mark.parametrize("name,P,Hq,Hkv,D,window", [
+    ("cfg1 llama-1B @512", 512, 32, 8, 64, 0),
+    ("cfg3b llama-3B @8192", 8192, 24, 8, 128, 0),
+    ("cfg4 gemma-1B global @32768", 32768, 4, 1, 256, 0),
+    ("cfg4 gemma-1B local W512 @32768", 32768, 4, 1, 256, 512),
+    ("cfg5 gemma-4B global @16640", 16640, 8, 4, 256, 0),
+    ("cfg5 gemma-4B local W1024", 16640, 8, 4, 256, 1024),
+    ("first token", 0, 24, 8, 128, 0),
+    ("window 1", 300, 8, 2, 64, 1),
+    ("odd length", 1001, 12, 4, 128, 0),
+    ("R=8", 2050, 32, 4, 64, 0),
+    ("R=5", 777, 10, 2, 128, 0),
+])
+def test_decode_f32_parity(gpu, name, P, Hq, Hkv, D, window):
+    print(f"[case] decode {name} P={P} Hq={Hq} Hkv={Hkv} D={D} W={window}", flush=True)
+    got, ref, _, _ = run_both(gpu, 10, P % 97, 1, P, Hq, Hkv, D, window)
+    assert rel_err(got, ref) <= DECODE_TOL
+
+
+@pytest.mark.parametrize("D", [2, 6, 48, 96, 160])
+def test_decode_generic_head_dims(gpu, D):
+    got, ref, _, _ = run_both(gpu, 11, D, 1, 123, 6, 3, D)
+    assert rel_err(got, ref) <= DECODE_TOL
+
+
+@pytest.mark.parametrize("name,S,P,Hq,Hkv,D,window", [
+    ("cfg2 llama-1B prefill", 512, 0, 32, 8, 64, 0),
+    ("cfg3a llama-3B prefill", 512, 0, 24, 8, 128, 0),
+    ("cfg4 gemma-1B prefill global", 300, 0, 4, 1, 256, 0),
+    ("cfg4 gemma-1B prefill local W64", 300, 0, 4, 1, 256, 64),
+    ("cfg5 gemma-4B chunk @4096", 128, 4096, 8, 4, 256, 0),
+    ("cfg5 gemma-4B chunk local W1024", 128, 4096, 8, 4, 256, 1024),
+    ("chunk with unaligned past", 45, 333, 24, 8, 128, 0),
+    ("two tokens", 2, 5, 8, 2, 64, 0),
+    ("33 tokens", 33, 0, 6, 2, 128, 0),
+    ("R=8", 70, 10, 32, 4, 64, 0),
+    ("R=1 MHA", 100, 3, 4, 4, 128, 0),
+])
+def test_prefill_bf16_parity(gpu, name, S, P, Hq, Hkv, D, window):
+    print(f"[case] prefill {name} S={S} P={P} Hq={Hq} Hkv={Hkv} D={D} W={window}", flush=True)
+    got, ref, _, _ = run_both(gpu, 12, S + P, S, P, Hq, Hkv, D, window)
+    assert rel_err(got, ref) <= BF16_TOL
+
+
+def test_prefill_non_causal(gpu):
+    got, ref, _, _ = run_both(gpu, 13, 0, 64, 20, 8, 2, 128, 0, causal=False)
+    assert rel_err(got, ref) <= BF16_TOL
+
+
+def test_prefill_f32_precision_path(gpu):
+    from spissa_amd import _ffi
+    from spissa_amd.device import Session  # noqa: F401
+
+    import ctypes
+
+    lib = _ffi.load()
+    h = ctypes.c_void_p()
+    assert lib.spissa_default_session(ctypes.byref(h)) == 0
+    assert lib.spissa_session_set_prefill_precision(h, _ffi.PREFILL_F32) == 0
+    try:
+        got, ref, _, _ = run_both(gpu, 14, 0, 200, 50, 24, 8, 128, 0)
+        assert rel_err(got, ref) <= F32_TOL
+    finally:
+        lib.spissa_session_set_prefill_precision(h, _ffi.PREFILL_BF16)
+
+
+def test_prefill_then_cache_append_then_decode_matches_full_recompute(gpu):
+    # tiny.rs:1801-1898 pattern: prefill + decode steps == full-context recompute per step.
+    Hq, Hkv, D, S0, steps = 8, 2, 64, 40, 5
+    n = S0 + steps
+    q, k, v, _, _ = layer_inputs(15, 0, n, 0, Hq, Hkv, D)
+    full = o.sdpa_with_cache(q, k, v, None, n, Hq, Hkv, D)
+    cache = gpu.KvCache(Hkv, D, n)
+    qw, kw = Hq * D, Hkv * D
+    out = gpu.scaled_dot_product_attention_with_cache(
+        q[:S0 * qw].copy(), k[:S0 * kw].copy(), v[:S0 * kw].copy(), cache, gpu.KvAttentionConfig(S0, Hq, Hkv, D, True))
+    cache.append(k[:S0 * kw].copy(), v[:S0 * kw].copy(), S0)
+    assert rel_err(out, full[:S0 * qw]) <= BF16_TOL
+    for t in range(S0, n):
+        qs, ks, vs = q[t * qw:(t + 1) * qw].copy(), k[t * kw:(t + 1) * kw].copy(), v[t * kw:(t + 1) * kw].copy()
+        got = gpu.scaled_dot_product_attention_with_cache(qs, ks, vs, cache, gpu.KvAttentionConfig(1, Hq, Hkv, D, True))
+        cache.append(ks, vs, 1)
+        assert rel_err(got, full[t * qw:(t + 1) * qw]) <= DECODE_TOL
+
+
+def test_reference_kats_through_the_gpu(gpu):
+    # rotary.rs:827-851 and ops.rs:537-554 through the drop-in entry points.
+    f = lambda *x: np.array(x, dtype=np.float32)
+    q_all, k_all, v_all = f(0.2, 0.7, -0.1, 0.4, 0.9, -0.3), f(0.5, -0.2, 0.1, 0.8, -0.4, 0.3), f(1.0, 0.0, -0.5, 2.0, 0.25, -1.0)
+    full = o.scaled_dot_product_attention(q_all, k_all, v_all, 3, 1, 2, True)
+    c = gpu.KvCache(1, 2, 3)
+    c.append(k_all[:4].copy(), v_all[:4].copy(), 2)
+    inc = gpu.scaled_dot_product_attention_with_cache(q_all[4:].copy(), k_all[4:].copy(), v_all[4:].copy(), c,
+                                                      gpu.KvAttentionConfig(1, 1, 1, 2, True))
+    np.testing.assert_allclose(inc, full[4:], atol=1e-6, rtol=0)
+    q = f(1.0, 0.0, 0.0, 1.0)
+    out = gpu.scaled_dot_product_attention(q, q.copy(), f(10.0, 0.0, 0.0, 20.0), 2, 1, 2, True)
+    np.testing.assert_allclose(out[:2], [10.0, 0.0], atol=1e-6)
+    assert 3.0 < out[2] < 3.4 and 13.0 < out[3] < 13.7
+
+
+def test_invalid_softmax_denominator_is_reported(gpu):
+    P, Hq, Hkv, D = 64, 8, 2, 128
+    q, k, v, pk, pv = layer_inputs(16, 0, 1, P, Hq, Hkv, D)
+    cache = gpu.KvCache(Hkv, D, P + 1)
+    cache.append(pk, pv, P)
+    q[5] = np.nan
+    with pytest.raises(gpu.InvalidTensorDataError):
+        gpu.scaled_dot_product_attention_with_cache(q, k, v, cache, gpu.KvAttentionConfig(1, Hq, Hkv, D, True))
+    # The session recovers: a valid call afterwards succeeds.
+    q[5] = 0.0
+    gpu.scaled_dot_product_attention_with_cache(q, k, v, cache, gpu.KvAttentionConfig(1, Hq, Hkv, D, True))
+
+
+def test_batched_decode_matches_per_sequence_oracle(gpu):
+    import torch
+
+    from spissa_amd.device import Session
+
+    B, Hq, Hkv, D = 16, 24, 8, 128
+    lens = [100 + 37 * b for b in range(B)]
+    s = Session(0)
+    caches, refs, qs, ks, vs = [], [], [], [], []
+    for b in range(B):
+        q, k, v, pk, pv = layer_inputs(17, 0, 1, lens[b], Hq, Hkv, D, sequence=b)
+        c = s.kv_cache(Hkv, D, lens[b] + 1)
+        c.append(pk, pv, lens[b])
+        rc = o.KvCache(Hkv, D, lens[b] + 1)
+        rc.append(pk, pv, lens[b])
+        refs.append(o.sdpa_with_cache(q, k, v, rc, 1, Hq, Hkv, D))
+        caches.append(c)
+        qs.append(q), ks.append(k), vs.append(v)
+    dq = torch.from_numpy(np.concatenate(qs)).cuda()
+    dk = torch.from_numpy(np.concatenate(ks)).cuda()
+    dv = torch.from_numpy(np.concatenate(vs)).cuda()
+    out = torch.empty_like(dq)
+    s.attention_decode_batch(dq, dk, dv, caches, gpu.KvAttentionConfig(1, Hq, Hkv, D, True), out)
+    s.sync()
+    got = out.cpu().numpy().reshape(B, -1)
+    for b in range(B):
+        assert rel_err(got[b], refs[b]) <= DECODE_TOL, b
