@@ -205,6 +205,19 @@ int spissa_attention_decode_batch_device(spissa_session *s, const float *d_q, co
                                          const float *d_v, const spissa_kv_cache *const *caches,
                                          size_t batch, const spissa_kv_attention_config *cfg,
                                          float *d_out);
+/* One fused decode step of one layer for `batch` sequences: the RoPE of q and
+ * k at position cache_len (rotary.rs:75-125 or 137-186, bit-identical to the
+ * drop-in RoPE), the attention of rotary.rs:335-415 with query_len == 1, and
+ * KvCache::append of the rotated key and the value (rotary.rs:226-256): the
+ * call sequence of models/llama/generate.rs:373-416 and
+ * models/gemma/generate.rs:247-295, in two kernel launches. d_q, d_k, d_v are
+ * read-only (rotated q and k are not written back). table may be NULL (no
+ * RoPE); otherwise it is a LLAMA or GEMMA table with rotary_dim == head_dim.
+ * Every cache gains one token; all capacity checks run before any launch. */
+int spissa_decode_step_device(spissa_session *s, const spissa_rope_table *table,
+                              const float *d_q, const float *d_k, const float *d_v,
+                              spissa_kv_cache *const *caches, size_t batch,
+                              const spissa_kv_attention_config *cfg, float *d_out);
 /* ops.rs:237-291 scaled_dot_product_attention (cacheless MHA, f32). */
 int spissa_scaled_dot_product_attention(const float *q, size_t q_len, const float *k,
                                         size_t k_len, const float *v, size_t v_len,

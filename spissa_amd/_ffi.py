@@ -121,6 +121,10 @@ SIGNATURES = {
         C.c_int,
         [c_void_p, c_void_p, c_void_p, c_void_p, C.POINTER(c_void_p), c_size,
          C.POINTER(AttnConfigC), c_void_p]),
+    "spissa_decode_step_device": (
+        C.c_int,
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, C.POINTER(c_void_p), c_size,
+         C.POINTER(AttnConfigC), c_void_p]),
     "spissa_scaled_dot_product_attention": (
         C.c_int,
         [c_float_p, c_size, c_float_p, c_size, c_float_p, c_size, c_size, c_size, c_size, C.c_int,

@@ -73,8 +73,7 @@ struct spissa_session {
   bool own_stream = false;
   int *d_err = nullptr;
   DevBuf io;        // drop-in host<->device staging
-  DevBuf partial;   // decode combine-tree entries
-  DevBuf counters;  // decode combine-tree counters (kept zero between launches)
+  DevBuf partial;   // decode split partials
   DevBuf stage;     // prefill bf16 staging of K / V^T
   DevBuf table;     // drop-in RoPE rows
   int prefill_precision = SPISSA_PREFILL_BF16;
@@ -154,7 +153,6 @@ extern "C" void spissa_session_destroy(spissa_session *s) {
   (void)hipStreamSynchronize(s->stream);
   free_buf(s->io);
   free_buf(s->partial);
-  free_buf(s->counters);
   free_buf(s->stage);
   free_buf(s->table);
   if (s->d_err) (void)hipFree(s->d_err);
@@ -858,9 +856,13 @@ static int pick_rb(int R) {
   return 1;
 }
 
+// Split-K decode over `batch` sequences (one new token each). Optionally fuses
+// the RoPE of q/k from `table` (rotate-half over the whole head) and the
+// append of the new key and value to each cache; the caller has validated
+// capacity when `append` is set.
 static int run_decode(spissa_session *s, const float *d_q, const float *d_k, const float *d_v,
                       const spissa_kv_cache *const *caches, size_t batch, const spissa_kv_attention_config *c,
-                      float *d_out) {
+                      float *d_out, const spissa_rope_table *table, bool append) {
   const int D = (int)c->head_dim, Hq = (int)c->num_heads, Hkv = (int)c->kv_heads;
   const int R = Hq / Hkv;
   const int RB = pick_rb(R);
@@ -877,25 +879,31 @@ static int run_decode(spissa_session *s, const float *d_q, const float *d_k, con
       a.seq[b].k = cb ? cb->keys : nullptr;
       a.seq[b].v = cb ? cb->values : nullptr;
       a.seq[b].past = P;
-      int keys = P + 1;
-      if (c->window > 0) keys = std::min<int>(keys, (int)c->window);
-      max_keys = std::max(max_keys, keys);
-      total_rows += (long)keys * Hkv * HB;
+      const int kstart = c->window > 0 ? std::max(0, P + 1 - (int)c->window) : 0;
+      const int cached = P - kstart;  // visible cached keys; the new token is handled apart
+      max_keys = std::max(max_keys, cached);
+      total_rows += (long)cached * Hkv * HB;
+      if (append) {
+        a.app_k[b] = cb->keys + (size_t)P * cb->width();
+        a.app_v[b] = cb->values + (size_t)P * cb->width();
+        a.app_kb[b] = cb->kb;
+        a.app_vt[b] = cb->vt;
+        a.app_cap[b] = (long)cb->shadow_cap;
+      }
     }
-    const int kps = decode_keys_per_split(D, RB, total_rows, max_keys);
+    const int kps = decode_keys_per_split(D, RB, total_rows, std::max(1, max_keys));
     const int max_splits = (max_keys + kps - 1) / kps;
-    const int entries = combine_tree_entries(max_splits);
-    const int ctrs = std::max(1, combine_tree_counters(max_splits));
     const size_t groups = (size_t)B * Hkv * HB;
-    ST_TRY(ensure_buf(s, s->partial, groups * entries * RB * (D + 2) * sizeof(float), false));
-    ST_TRY(ensure_buf(s, s->counters, groups * ctrs * sizeof(int), true));
-    a.q = d_q + b0 * (size_t)Hq * D;
-    a.cur_k = d_k + b0 * (size_t)Hkv * D;
+    ST_TRY(ensure_buf(s, s->partial, groups * std::max(1, max_splits) * RB * (D + 2) * sizeof(float), false));
+    a.q = const_cast<float *>(d_q) + b0 * (size_t)Hq * D;
+    a.cur_k = const_cast<float *>(d_k) + b0 * (size_t)Hkv * D;
     a.cur_v = d_v + b0 * (size_t)Hkv * D;
     a.out = d_out + b0 * (size_t)Hq * D;
     a.partial = (float *)s->partial.p;
-    a.counters = (int *)s->counters.p;
     a.err = s->d_err;
+    a.rope_cos = table ? table->cos : nullptr;
+    a.rope_sin = table ? table->sin : nullptr;
+    a.do_append = append ? 1 : 0;
     a.B = B;
     a.Hq = Hq;
     a.Hkv = Hkv;
@@ -903,10 +911,9 @@ static int run_decode(spissa_session *s, const float *d_q, const float *d_k, con
     a.HB = HB;
     a.window = (int)c->window;
     a.kps = kps;
-    a.max_entries = entries;
-    a.max_counters = ctrs;
+    a.max_splits = max_splits;
     a.qscale = (1.0f / sqrtf((float)D)) * 1.4426950408889634f;
-    HIP_TRY(launch_decode(s->stream, a, D, RB, max_splits));
+    HIP_TRY(launch_decode(s->stream, a, D, RB));
   }
   return SPISSA_OK;
 }
@@ -981,7 +988,8 @@ static int attention_device_impl(spissa_session *s, const float *d_q, const floa
   HIP_TRY(hipSetDevice(s->device));
   const int D = (int)c->head_dim;
   const int R = (int)(c->num_heads / c->kv_heads);
-  if (c->query_len == 1 && decode_supported(D, R)) return run_decode(s, d_q, d_k, d_v, &cache, 1, c, d_out);
+  if (c->query_len == 1 && decode_supported(D, R))
+    return run_decode(s, d_q, d_k, d_v, &cache, 1, c, d_out, nullptr, false);
   if (c->query_len > 1 && s->prefill_precision == SPISSA_PREFILL_BF16 && prefill_supported(D))
     return run_prefill(s, d_q, d_k, d_v, const_cast<spissa_kv_cache *>(cache), c, d_out);
   return run_generic(s, d_q, d_k, d_v, cache, c, d_out);
@@ -1011,11 +1019,44 @@ extern "C" int spissa_attention_decode_batch_device(spissa_session *s, const flo
   HIP_TRY(hipSetDevice(s->device));
   const int D = (int)cfg->head_dim;
   const int R = (int)(cfg->num_heads / cfg->kv_heads);
-  if (decode_supported(D, R)) return run_decode(s, d_q, d_k, d_v, caches, batch, cfg, d_out);
+  if (decode_supported(D, R)) return run_decode(s, d_q, d_k, d_v, caches, batch, cfg, d_out, nullptr, false);
   for (size_t b = 0; b < batch; ++b) {
     const size_t qo = b * cfg->num_heads * cfg->head_dim, ko = b * cfg->kv_heads * cfg->head_dim;
     ST_TRY(run_generic(s, d_q + qo, d_k + ko, d_v + ko, caches ? caches[b] : nullptr, cfg, d_out + qo));
   }
+  return SPISSA_OK;
+  GUARD_END
+}
+
+extern "C" int spissa_decode_step_device(spissa_session *s, const spissa_rope_table *table, const float *d_q,
+                                         const float *d_k, const float *d_v, spissa_kv_cache *const *caches,
+                                         size_t batch, const spissa_kv_attention_config *cfg, float *d_out) {
+  GUARD_BEGIN
+  if (!s || !cfg || !caches) return set_err(SPISSA_ERR_ARGUMENT, "null argument");
+  if (cfg->query_len != 1) return set_err(SPISSA_ERR_SHAPE, "a decode step needs query_len == 1, got %zu", cfg->query_len);
+  for (size_t b = 0; b < batch; ++b) {
+    if (!caches[b]) return set_err(SPISSA_ERR_ARGUMENT, "cache %zu is null", b);
+    ST_TRY(validate_attention(0, 0, 0, caches[b], cfg, false));
+    size_t n, nl;  // rotary.rs:227-251: the append must fit before anything runs
+    ST_TRY(kv_validate_append(caches[b], 0, 0, 1, false, &n, &nl));
+    if (caches[b]->session->device != s->device)
+      return set_err(SPISSA_ERR_ARGUMENT, "cache %zu lives on another device", b);
+  }
+  const int D = (int)cfg->head_dim;
+  if (!decode_supported(D, (int)(cfg->num_heads / cfg->kv_heads)))
+    return set_err(SPISSA_ERR_SHAPE, "the fused decode step supports head_dim 64, 128 and 256, got %d", D);
+  if (table) {
+    if (table->kind == SPISSA_ROPE_NEOX || table->rotary_dim != cfg->head_dim)
+      return set_err(SPISSA_ERR_SHAPE, "the fused decode step needs a llama or gemma table over the whole head");
+    for (size_t b = 0; b < batch; ++b)
+      if (caches[b]->len >= table->max_positions)
+        return set_err(SPISSA_ERR_SHAPE, "position %zu exceeds the rope table (%zu positions)", caches[b]->len,
+                       table->max_positions);
+  }
+  if (batch == 0) return SPISSA_OK;
+  HIP_TRY(hipSetDevice(s->device));
+  ST_TRY(run_decode(s, d_q, d_k, d_v, caches, batch, cfg, d_out, table, true));
+  for (size_t b = 0; b < batch; ++b) caches[b]->len += 1;
   return SPISSA_OK;
   GUARD_END
 }

@@ -1,29 +1,35 @@
 // decode.hip -- single-token f32 attention against the resident KV cache
 // (rotary.rs:335-415 with query_len == 1), as split-K flash-decoding for gfx950.
 //
-// Work split. One workgroup (256 threads, 4 waves) owns a range of keys
-// ("split") of one KV head for one sequence and serves RB query heads of that
-// KV head's group, so each K/V row is read from HBM once per head block. A key
-// row (D floats) is spread over LPR = D/8 lanes, each lane holding two float4
-// (dims [4*sub, 4*sub+4) and [D/2 + 4*sub, ...)), so each load instruction
-// moves contiguous 16*LPR-byte pieces of rows. A wave therefore streams 64/LPR
-// rows at once, the workgroup NG = 4*64/LPR rows, and every lane keeps RPG rows
-// of K and V in flight per iteration.
+// Two kernels per launch:
 //
-// Scores. The lane's 8-element partial dot is reduced over the row's LPR lanes
-// with DPP (quad_perm, row_half_mirror, row_mirror) and the gfx950
-// v_permlane16_swap / v_permlane32_swap exchanges: all-reduce, no LDS.
+// 1. decode_split_kernel covers the cached keys only. One workgroup
+//    (256 threads, 4 waves) owns a range of cached keys ("split") of one KV
+//    head for one sequence and serves RB query heads of that head's group, so
+//    every K/V row is read from HBM once per head block. A key row (D floats)
+//    is spread over LPR = D/8 lanes; a lane holds two float4 (dims
+//    [4*sub, 4*sub+4) and [D/2 + 4*sub, ...)), so each load instruction of a
+//    lane group moves a contiguous 16*LPR-byte piece of a row, and the lane's
+//    two float4 are exactly rotate-half partners (RoPE of q is lane-local).
+//    The 8-element partial dots are all-reduced over the row's LPR lanes with
+//    DPP (quad_perm, row_half_mirror, row_mirror) and the gfx950
+//    v_permlane16/32_swap exchanges; each row group runs an online softmax in
+//    the log2 domain; the groups of a wave merge in registers (DPP row_ror:8,
+//    permlane swaps), the four waves through one LDS exchange, and every
+//    workgroup stores its partial (max, sum, unnormalised output).
 //
-// Softmax. Each row group runs its own online softmax in the log2 domain
-// (the scale 1/sqrt(D)*log2(e) is folded into q). Groups are merged through
-// LDS at the end of the workgroup, splits are merged by a combine tree: the
-// last-arriving workgroup of every kCombineFanIn siblings (atomic arrival
-// counter) merges their partial (max, sum, output) entries, up to the root,
-// which writes the normalised output. Counters reset themselves, so
-// consecutive launches need no memset.
+// 2. decode_combine_kernel handles the new token itself (its optional RoPE,
+//    its score and value), merges it with the splits' partials into the
+//    normalised output, and optionally appends the new (rotated) key and
+//    value to the cache row it occupies. The kernel boundary publishes the
+//    partials across XCDs, so no in-kernel device-scope synchronisation is
+//    needed, and a whole decode step of a layer (RoPE, attention, append) is
+//    these two launches.
 //
 // Errors. A zero or non-finite softmax denominator (rotary.rs:560-564) sets a
 // device error bit instead of aborting.
+#include <cstdlib>
+
 #include "internal.hpp"
 
 namespace spissa {
@@ -35,26 +41,35 @@ __device__ __forceinline__ float dpp(float v) {
   return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xf, 0xf, false);
 }
 
-// Sum / max of v with the value of lane ^ 16 (v_permlane16_swap_b32).
-__device__ __forceinline__ float swap16_sum(float v) {
+// Value of lane ^ 16 (v_permlane16_swap_b32) and of lane ^ 32 (v_permlane32_swap_b32).
+__device__ __forceinline__ float xor16(float v) {
   auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
 }
-__device__ __forceinline__ float swap32_sum(float v) {
+__device__ __forceinline__ float xor32(float v) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
+// Value of lane ^ 8 (DPP row_ror:8 within each 16-lane row).
+__device__ __forceinline__ float xor8(float v) { return dpp<0x128>(v); }
+
+template <int M>
+__device__ __forceinline__ float lane_xor(float v) {
+  if constexpr (M == 8) return xor8(v);
+  else if constexpr (M == 16) return xor16(v);
+  else return xor32(v);
 }
 
 // All-reduce (sum) over aligned groups of LPR lanes.
 template <int LPR>
 __device__ __forceinline__ float group_sum(float v) {
   static_assert(LPR >= 2 && LPR <= 64 && (LPR & (LPR - 1)) == 0, "LPR");
-  v += dpp<0xB1>(v);                              // lane ^ 1  (quad_perm [1,0,3,2])
-  if constexpr (LPR >= 4) v += dpp<0x4E>(v);      // lane ^ 2  (quad_perm [2,3,0,1])
-  if constexpr (LPR >= 8) v += dpp<0x141>(v);     // quad <-> quad (row_half_mirror)
-  if constexpr (LPR >= 16) v += dpp<0x140>(v);    // 8 <-> 8 (row_mirror)
-  if constexpr (LPR >= 32) v = swap16_sum(v);     // row <-> row
-  if constexpr (LPR >= 64) v = swap32_sum(v);     // half <-> half
+  v += dpp<0xB1>(v);                           // lane ^ 1  (quad_perm [1,0,3,2])
+  if constexpr (LPR >= 4) v += dpp<0x4E>(v);   // lane ^ 2  (quad_perm [2,3,0,1])
+  if constexpr (LPR >= 8) v += dpp<0x141>(v);  // quad <-> quad (row_half_mirror)
+  if constexpr (LPR >= 16) v += dpp<0x140>(v); // 8 <-> 8 (row_mirror)
+  if constexpr (LPR >= 32) v += xor16(v);      // row <-> row
+  if constexpr (LPR >= 64) v += xor32(v);      // half <-> half
   return v;
 }
 
@@ -82,71 +97,102 @@ __device__ __forceinline__ float4 fma4(float p, float4 v, float4 acc) {
   return make_float4(fmaf(p, v.x, acc.x), fmaf(p, v.y, acc.y), fmaf(p, v.z, acc.z),
                      fmaf(p, v.w, acc.w));
 }
+__device__ __forceinline__ float4 axpby4(float4 x, float a, float4 y, float b) {
+  return make_float4(x.x * a + y.x * b, x.y * a + y.y * b, x.z * a + y.z * b, x.w * a + y.w * b);
+}
+
+constexpr float NEG_INF = -__builtin_inff();
+
+__device__ __forceinline__ float safe_max(float m) { return m == NEG_INF ? 0.0f : m; }
+
+// rotary.rs:467-481 on one (first, second) pair, each product rounded
+// separately, so the result is bit-identical to the reference rotation.
+__device__ __forceinline__ void rotate_pair(float &first, float &second, float c, float s) {
+#pragma clang fp contract(off)
+  const float a = first * c - second * s;
+  const float b = second * c + first * s;
+  first = a;
+  second = b;
+}
+
+// Merges the online-softmax state of this lane with lane ^ M (same dims, other row group).
+template <int RB, int M>
+__device__ __forceinline__ void merge_with(float (&m)[RB], float (&l)[RB], float4 (&o)[RB][2]) {
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    const float mp = lane_xor<M>(m[r]);
+    const float lp = lane_xor<M>(l[r]);
+    float4 op0, op1;
+    op0.x = lane_xor<M>(o[r][0].x); op0.y = lane_xor<M>(o[r][0].y);
+    op0.z = lane_xor<M>(o[r][0].z); op0.w = lane_xor<M>(o[r][0].w);
+    op1.x = lane_xor<M>(o[r][1].x); op1.y = lane_xor<M>(o[r][1].y);
+    op1.z = lane_xor<M>(o[r][1].z); op1.w = lane_xor<M>(o[r][1].w);
+    const float mn = fmaxf(m[r], mp);
+    const float ms = safe_max(mn);
+    const float fa = fast_exp2(m[r] - ms), fb = fast_exp2(mp - ms);
+    l[r] = l[r] * fa + lp * fb;
+    o[r][0] = axpby4(o[r][0], fa, op0, fb);
+    o[r][1] = axpby4(o[r][1], fa, op1, fb);
+    m[r] = mn;
+  }
+}
 
 }  // namespace
 
-int combine_tree_entries(int n) {
-  int total = n;
-  while (n > 1) {
-    int groups = (n + kCombineFanIn - 1) / kCombineFanIn;
-    if (groups > 1) total += groups;
-    n = groups;
-  }
-  return total;
-}
-
-int combine_tree_counters(int n) {
-  int total = 0;
-  while (n > 1) {
-    int groups = (n + kCombineFanIn - 1) / kCombineFanIn;
-    total += groups;
-    n = groups;
-  }
-  return total;
-}
-
+// At least 4 waves per SIMD (<= 128 VGPRs): four workgroups per CU stay resident.
 template <int D, int RB, int RPG>
-__global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
+__global__ __launch_bounds__(256, 4) void decode_split_kernel(const DecodeArgs a) {
   constexpr int LPR = D / 8;
-  constexpr int GPW = 64 / LPR;
-  constexpr int NG = 4 * GPW;
+  constexpr int GPW = 64 / LPR;  // row groups per wave
+  constexpr int NG = 4 * GPW;    // row groups per workgroup
   constexpr int HALF = D / 2;
   constexpr int ENTRY = RB * (D + 2);  // O[RB][D] then (max, sum)[RB]
-  constexpr float NEG_INF = -__builtin_inff();
 
-  __shared__ float red_o[NG][RB][D];
-  __shared__ float red_m[NG][RB];
-  __shared__ float red_l[NG][RB];
-  __shared__ float fac[NG > kCombineFanIn ? NG : kCombineFanIn][RB];
-  __shared__ float s_max[RB];
-  __shared__ float s_sum[RB];
-  __shared__ int s_last;
+  __shared__ float w_o[4][RB][D];
+  __shared__ float w_ml[4][RB][2];
 
-  const int split = blockIdx.x;
-  const int hb = blockIdx.y % a.HB;
-  const int h = blockIdx.y / a.HB;
+  // Head blocks are the fastest grid dimension: the workgroups that read the
+  // same key rows (all KV heads of one split) are dispatched back to back.
+  const int split = blockIdx.y;
+  const int hb = blockIdx.x % a.HB;
+  const int h = blockIdx.x / a.HB;
   const int b = blockIdx.z;
   const int P = a.seq[b].past;
-  const int kend = P + 1;
-  const int kstart = a.window > 0 ? max(0, kend - a.window) : 0;
-  const int nsplit = (kend - kstart + a.kps - 1) / a.kps;
+  const int kstart = a.window > 0 ? max(0, P + 1 - a.window) : 0;
+  const int nsplit = (P - kstart + a.kps - 1) / a.kps;  // cached keys only
   if (split >= nsplit) return;
   const int k0 = kstart + split * a.kps;
-  const int k1 = min(kend, k0 + a.kps);
+  const int k1 = min(P, k0 + a.kps);
 
   const int tid = threadIdx.x;
+  const int wave = tid >> 6;
   const int lane = tid & 63;
   const int sub = lane % LPR;
-  const int grp = (tid >> 6) * GPW + lane / LPR;
+  const int grp = wave * GPW + lane / LPR;
   const int qh0 = h * a.R + hb * RB;
+
+  const long row_stride = (long)a.Hkv * D;
+  const float *kcache = a.seq[b].k + (long)h * D;
+  const float *vcache = a.seq[b].v + (long)h * D;
 
   float4 qv[RB][2];
   {
     const float *qb = a.q + ((long)b * a.Hq + qh0) * D;
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
-      qv[r][0] = scale4(ld4(qb + r * D + 4 * sub), a.qscale);
-      qv[r][1] = scale4(ld4(qb + r * D + HALF + 4 * sub), a.qscale);
+      qv[r][0] = ld4(qb + r * D + 4 * sub);
+      qv[r][1] = ld4(qb + r * D + HALF + 4 * sub);
+    }
+    if (a.rope_cos) {
+      const float4 c = ld4(a.rope_cos + (long)P * HALF + 4 * sub);
+      const float4 sn = ld4(a.rope_sin + (long)P * HALF + 4 * sub);
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        rotate_pair(qv[r][0].x, qv[r][1].x, c.x, sn.x);
+        rotate_pair(qv[r][0].y, qv[r][1].y, c.y, sn.y);
+        rotate_pair(qv[r][0].z, qv[r][1].z, c.z, sn.z);
+        rotate_pair(qv[r][0].w, qv[r][1].w, c.w, sn.w);
+      }
     }
   }
   float m[RB], l[RB];
@@ -159,12 +205,6 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
     o[r][1] = o[r][0];
   }
 
-  const long row_stride = (long)a.Hkv * D;
-  const float *kcache = a.seq[b].k;
-  const float *vcache = a.seq[b].v;
-  const float *knew = a.cur_k + ((long)b * a.Hkv + h) * D;
-  const float *vnew = a.cur_v + ((long)b * a.Hkv + h) * D;
-
   for (int c = k0; c < k1; c += NG * RPG) {
     float4 kr[RPG][2], vr[RPG][2];
     bool valid[RPG];
@@ -173,11 +213,8 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
       const int j = c + grp + i * NG;
       valid[i] = j < k1;
       if (valid[i]) {
-        const float *kp = knew, *vp = vnew;
-        if (j < P) {
-          kp = kcache + (long)j * row_stride + (long)h * D;
-          vp = vcache + (long)j * row_stride + (long)h * D;
-        }
+        const float *kp = kcache + (long)j * row_stride;
+        const float *vp = vcache + (long)j * row_stride;
         kr[i][0] = ld4(kp + 4 * sub);
         kr[i][1] = ld4(kp + HALF + 4 * sub);
         vr[i][0] = ld4(vp + 4 * sub);
@@ -191,7 +228,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
     for (int i = 0; i < RPG; ++i) {
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
-        float s = group_sum<LPR>(dot8(qv[r][0], qv[r][1], kr[i][0], kr[i][1]));
+        const float s = group_sum<LPR>(dot8(qv[r][0], qv[r][1], kr[i][0], kr[i][1])) * a.qscale;
         sc[i][r] = valid[i] ? s : NEG_INF;
       }
     }
@@ -200,7 +237,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
       float mx = m[r];
 #pragma unroll
       for (int i = 0; i < RPG; ++i) mx = fmaxf(mx, sc[i][r]);
-      const float ms = mx == NEG_INF ? 0.0f : mx;
+      const float ms = safe_max(mx);
       const float alpha = fast_exp2(m[r] - ms);
       l[r] *= alpha;
       o[r][0] = scale4(o[r][0], alpha);
@@ -216,159 +253,198 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
     }
   }
 
-  // ---- merge the NG row groups of this workgroup ----
+  // ---- merge the row groups of each wave in registers ----
+  if constexpr (GPW >= 8) merge_with<RB, 8>(m, l, o);
+  if constexpr (GPW >= 4) merge_with<RB, 16>(m, l, o);
+  if constexpr (GPW >= 2) merge_with<RB, 32>(m, l, o);
+  // Lanes of row group 0 now hold the wave's state; merge the four waves in LDS.
+  if (lane < LPR) {
 #pragma unroll
-  for (int r = 0; r < RB; ++r) {
-    *reinterpret_cast<float4 *>(&red_o[grp][r][4 * sub]) = o[r][0];
-    *reinterpret_cast<float4 *>(&red_o[grp][r][HALF + 4 * sub]) = o[r][1];
-    if (sub == 0) {
-      red_m[grp][r] = m[r];
-      red_l[grp][r] = l[r];
+    for (int r = 0; r < RB; ++r) {
+      *reinterpret_cast<float4 *>(&w_o[wave][r][4 * sub]) = o[r][0];
+      *reinterpret_cast<float4 *>(&w_o[wave][r][HALF + 4 * sub]) = o[r][1];
+      if (sub == 0) {
+        w_ml[wave][r][0] = m[r];
+        w_ml[wave][r][1] = l[r];
+      }
     }
-  }
-  __syncthreads();
-  if (tid < RB) {
-    float M = NEG_INF;
-    for (int g = 0; g < NG; ++g) M = fmaxf(M, red_m[g][tid]);
-    s_max[tid] = M;
-  }
-  __syncthreads();
-  if (tid < NG * RB) {
-    const int g = tid / RB, r = tid % RB;
-    const float M = s_max[r];
-    fac[g][r] = fast_exp2(red_m[g][r] - (M == NEG_INF ? 0.0f : M));
-  }
-  __syncthreads();
-  if (tid < RB) {
-    float L = 0.0f;
-    for (int g = 0; g < NG; ++g) L += red_l[g][tid] * fac[g][tid];
-    s_sum[tid] = L;
-  }
-  // Each thread owns outputs e = tid + 256*u of the RB*D block.
-  constexpr int PER = (RB * D + 255) / 256;
-  float acc[PER];
-#pragma unroll
-  for (int u = 0; u < PER; ++u) {
-    const int e = tid + 256 * u;
-    float s = 0.0f;
-    if (e < RB * D) {
-      const int r = e / D, dim = e % D;
-      for (int g = 0; g < NG; ++g) s += red_o[g][r][dim] * fac[g][r];
-    }
-    acc[u] = s;
   }
   __syncthreads();
 
   const long bhh = ((long)b * a.Hkv + h) * a.HB + hb;
-  float *out = a.out + ((long)b * a.Hq + qh0) * D;
-
-  auto finalize = [&]() {
+  float *dst = a.partial + (bhh * a.max_splits + split) * (long)ENTRY;
+  for (int e = tid; e < RB * D; e += 256) {
+    const int r = e / D;
+    const float M = fmaxf(fmaxf(w_ml[0][r][0], w_ml[1][r][0]), fmaxf(w_ml[2][r][0], w_ml[3][r][0]));
+    const float Ms = safe_max(M);
+    float L = 0.0f, O = 0.0f;
 #pragma unroll
-    for (int u = 0; u < PER; ++u) {
-      const int e = tid + 256 * u;
-      if (e < RB * D) {
-        const float L = s_sum[e / D];
-        out[e] = acc[u] / L;
-        if ((e % D) == 0 && !(L > 0.0f && L < __builtin_inff())) atomicOr(a.err, kDevErrSoftmaxDenominator);
-      }
+    for (int w = 0; w < 4; ++w) {
+      const float f = fast_exp2(w_ml[w][r][0] - Ms);
+      L += w_ml[w][r][1] * f;
+      O += w_o[w][r][e % D] * f;
     }
-  };
+    dst[e] = O;
+    if ((e % D) == 0) {
+      dst[RB * D + 2 * r] = M;
+      dst[RB * D + 2 * r + 1] = L;
+    }
+  }
+}
 
-  if (nsplit == 1) {
-    finalize();
-    return;
+// Finishes the attention of one (sequence, KV head, head block): the new
+// token's score and value, merged with the partials of every split of the
+// cached keys, then the optional append of the new key and value.
+// Grid: (RB*D / 64, Hkv*HB, B); 1024 threads = 64 consecutive outputs x 16
+// split lanes. Each lane keeps an online (max, sum, output) over its splits
+// with the loads of four splits in flight; the 16 lanes of every output are
+// merged through LDS.
+template <int D, int RB>
+__global__ __launch_bounds__(1024) void decode_combine_kernel(const DecodeArgs a) {
+  constexpr int HALF = D / 2;
+  constexpr int ENTRY = RB * (D + 2);
+  constexpr int OUTS = 64, SL = 16, UNROLL = 4;
+  __shared__ float s_m[SL][OUTS], s_l[SL][OUTS], s_o[SL][OUTS];
+  __shared__ float s_dot[RB * D / 64];
+  __shared__ float s_new[RB];
+
+  const int hb = blockIdx.y % a.HB;
+  const int h = blockIdx.y / a.HB;
+  const int b = blockIdx.z;
+  const int P = a.seq[b].past;
+  const int kstart = a.window > 0 ? max(0, P + 1 - a.window) : 0;
+  const int nsplit = (P - kstart + a.kps - 1) / a.kps;
+  const int tid = threadIdx.x;
+  const int out = tid & (OUTS - 1);
+  const int sl = tid / OUTS;
+  const int e = blockIdx.x * OUTS + out;  // < RB*D: RB*D is a multiple of 64
+  const int r = e / D;
+  const int qh0 = h * a.R + hb * RB;
+  const float *knew = a.cur_k + ((long)b * a.Hkv + h) * D;
+  const float *vnew = a.cur_v + ((long)b * a.Hkv + h) * D;
+
+  // ---- the new token: (rotated) q . (rotated) k for the RB query heads ----
+  float kd = 0.0f;  // this thread's (rotated) key element, kept for the append
+  if (tid < RB * D) {
+    const int rr = tid / D, d = tid % D;
+    const float *qrow = a.q + ((long)b * a.Hq + qh0 + rr) * D;
+    float qd = qrow[d];
+    kd = knew[d];
+    if (a.rope_cos) {
+      const int pair = d % HALF;
+      const float c = a.rope_cos[(long)P * HALF + pair], sn = a.rope_sin[(long)P * HALF + pair];
+      float q1 = qrow[pair], q2 = qrow[pair + HALF], k1 = knew[pair], k2 = knew[pair + HALF];
+      rotate_pair(q1, q2, c, sn);
+      rotate_pair(k1, k2, c, sn);
+      qd = d < HALF ? q1 : q2;
+      kd = d < HALF ? k1 : k2;
+    }
+    float prod = qd * kd;
+    prod = group_sum<64>(prod);
+    if ((tid & 63) == 0) s_dot[tid >> 6] = prod;
   }
 
-  float *ebase = a.partial + bhh * (long)a.max_entries * ENTRY;
-  int *cbase = a.counters + bhh * a.max_counters;
-  auto write_entry = [&](int slot) {
-    float *ent = ebase + (long)slot * ENTRY;
+  // ---- the cached keys: partials of the splits ----
+  const long bhh = ((long)b * a.Hkv + h) * a.HB + hb;
+  const float *ents = a.partial + bhh * a.max_splits * (long)ENTRY;
+  float m = NEG_INF, l = 0.0f, o = 0.0f;
+  for (int s0 = sl; s0 < nsplit; s0 += SL * UNROLL) {
+    float ms[UNROLL], ls[UNROLL], os[UNROLL];
 #pragma unroll
-    for (int u = 0; u < PER; ++u) {
-      const int e = tid + 256 * u;
-      if (e < RB * D) ent[e] = acc[u];
-    }
-    if (tid < RB) {
-      ent[RB * D + 2 * tid] = s_max[tid];
-      ent[RB * D + 2 * tid + 1] = s_sum[tid];
-    }
-  };
-
-  int n = nsplit, idx = split, eoff = 0, coff = 0;
-  write_entry(idx);
-  while (n > 1) {
-    const int groups = (n + kCombineFanIn - 1) / kCombineFanIn;
-    const int g = idx / kCombineFanIn;
-    const int first = g * kCombineFanIn;
-    const int cnt = min(kCombineFanIn, n - first);
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-      const int old = atomicAdd(&cbase[coff + g], 1);
-      s_last = (old == cnt - 1);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    if (tid == 0) atomicExch(&cbase[coff + g], 0);
-    const float *ents = ebase + (long)(eoff + first) * ENTRY;
-    if (tid < RB) {
-      float M = NEG_INF;
-      for (int k = 0; k < cnt; ++k) M = fmaxf(M, ents[(long)k * ENTRY + RB * D + 2 * tid]);
-      s_max[tid] = M;
-    }
-    __syncthreads();
-    if (tid < cnt * RB) {
-      const int k = tid / RB, r = tid % RB;
-      const float M = s_max[r];
-      fac[k][r] = fast_exp2(ents[(long)k * ENTRY + RB * D + 2 * r] - (M == NEG_INF ? 0.0f : M));
-    }
-    __syncthreads();
-    if (tid < RB) {
-      float L = 0.0f;
-      for (int k = 0; k < cnt; ++k) L += ents[(long)k * ENTRY + RB * D + 2 * tid + 1] * fac[k][tid];
-      s_sum[tid] = L;
-    }
-#pragma unroll
-    for (int u = 0; u < PER; ++u) {
-      const int e = tid + 256 * u;
-      float s = 0.0f;
-      if (e < RB * D) {
-        const int r = e / D;
-        for (int k = 0; k < cnt; ++k) s += ents[(long)k * ENTRY + e] * fac[k][r];
+    for (int u = 0; u < UNROLL; ++u) {
+      const int s = s0 + u * SL;
+      if (s < nsplit) {
+        const float *ent = ents + (long)s * ENTRY;
+        ms[u] = ent[RB * D + 2 * r];
+        ls[u] = ent[RB * D + 2 * r + 1];
+        os[u] = ent[e];
+      } else {
+        ms[u] = NEG_INF;
+        ls[u] = 0.0f;
+        os[u] = 0.0f;
       }
-      acc[u] = s;
     }
-    __syncthreads();
-    if (groups == 1) {
-      finalize();
-      return;
+    float mx = m;
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) mx = fmaxf(mx, ms[u]);
+    const float mxs = safe_max(mx);
+    const float f = fast_exp2(m - mxs);
+    l *= f;
+    o *= f;
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const float g = fast_exp2(ms[u] - mxs);
+      l += ls[u] * g;
+      o += os[u] * g;
     }
-    eoff += n;
-    coff += groups;
-    idx = g;
-    n = groups;
-    write_entry(eoff + idx);
+    m = mx;
+  }
+  s_m[sl][out] = m;
+  s_l[sl][out] = l;
+  s_o[sl][out] = o;
+  __syncthreads();
+  if (tid < RB) {
+    float dot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < D / 64; ++w) dot += s_dot[tid * (D / 64) + w];
+    s_new[tid] = dot * a.qscale;
+  }
+  __syncthreads();
+  if (sl == 0) {
+    const float sn = s_new[r];
+    float M = sn;
+#pragma unroll
+    for (int k = 0; k < SL; ++k) M = fmaxf(M, s_m[k][out]);
+    const float Ms = safe_max(M);
+    const float pn = fast_exp2(sn - Ms);
+    float L = pn, O = pn * vnew[e % D];
+#pragma unroll
+    for (int k = 0; k < SL; ++k) {
+      const float g = fast_exp2(s_m[k][out] - Ms);
+      L += s_l[k][out] * g;
+      O += s_o[k][out] * g;
+    }
+    a.out[((long)b * a.Hq + qh0) * D + e] = O / L;
+    if ((e % D) == 0 && !(L > 0.0f && L < __builtin_inff())) atomicOr(a.err, kDevErrSoftmaxDenominator);
+  }
+  // ---- append the new (rotated) key and value at cache row P ----
+  if (a.do_append && blockIdx.x == 0 && hb == 0 && tid < D) {
+    const float vd = vnew[tid];
+    a.app_k[b][(long)h * D + tid] = kd;
+    a.app_v[b][(long)h * D + tid] = vd;
+    if (a.app_kb[b]) {
+      const long cap = a.app_cap[b];
+      a.app_kb[b][((long)h * cap + P) * D + tid] = (bf16)kd;
+      a.app_vt[b][((long)h * D + tid) * cap + P] = (bf16)vd;
+    }
   }
 }
 
 namespace {
-constexpr int kRowsPerGroup = 4;
+// Rows per lane group in flight: four, three for four query heads per block
+// (keeps the split kernel within 128 VGPRs without spills).
+constexpr int rows_per_group(int RB) { return RB >= 4 ? 3 : 4; }
 
 template <int D, int RB>
-hipError_t launch_one(hipStream_t st, const DecodeArgs &a, int max_splits) {
-  dim3 grid((unsigned)max_splits, (unsigned)(a.Hkv * a.HB), (unsigned)a.B);
-  hipLaunchKernelGGL((decode_kernel<D, RB, kRowsPerGroup>), grid, dim3(256), 0, st, a);
+hipError_t launch_one(hipStream_t st, const DecodeArgs &a) {
+  if (a.max_splits > 0) {
+    dim3 grid((unsigned)(a.Hkv * a.HB), (unsigned)a.max_splits, (unsigned)a.B);
+    hipLaunchKernelGGL((decode_split_kernel<D, RB, rows_per_group(RB)>), grid, dim3(256), 0, st, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  dim3 cgrid((unsigned)(RB * D / 64), (unsigned)(a.Hkv * a.HB), (unsigned)a.B);
+  hipLaunchKernelGGL((decode_combine_kernel<D, RB>), cgrid, dim3(1024), 0, st, a);
   return hipGetLastError();
 }
 
 template <int D>
-hipError_t launch_d(hipStream_t st, const DecodeArgs &a, int RB, int max_splits) {
+hipError_t launch_d(hipStream_t st, const DecodeArgs &a, int RB) {
   switch (RB) {
-    case 1: return launch_one<D, 1>(st, a, max_splits);
-    case 2: return launch_one<D, 2>(st, a, max_splits);
-    case 3: return launch_one<D, 3>(st, a, max_splits);
-    case 4: return launch_one<D, 4>(st, a, max_splits);
+    case 1: return launch_one<D, 1>(st, a);
+    case 2: return launch_one<D, 2>(st, a);
+    case 3: return launch_one<D, 3>(st, a);
+    case 4: return launch_one<D, 4>(st, a);
     default: return hipErrorInvalidValue;
   }
 }
@@ -377,27 +453,25 @@ hipError_t launch_d(hipStream_t st, const DecodeArgs &a, int RB, int max_splits)
 bool decode_supported(int D, int R) { return (D == 64 || D == 128 || D == 256) && R >= 1; }
 
 int decode_keys_per_split(int D, int RB, long total_rows, int max_keys) {
-  (void)RB;
-  const int chunk = 4 * (64 / (D / 8)) * kRowsPerGroup;  // keys one workgroup iteration covers
-  static long target = [] {
+  const int chunk = 4 * (64 / (D / 8)) * rows_per_group(RB);  // keys of one workgroup iteration
+  static const long target = [] {
     const char *env = getenv("SPISSA_DECODE_TARGET_WGS");
-    long v = env ? atol(env) : 0;
-    return v > 0 ? v : 2048L;
+    const long v = env ? atol(env) : 0;
+    return v > 0 ? v : 1024L;
   }();
-  long per = (total_rows + target - 1) / target;
-  long iters = (per + chunk - 1) / chunk;
-  if (iters < 1) iters = 1;
-  long kps = iters * chunk;
-  // Keep the combine tree shallow: at most kCombineFanIn^2 splits per (sequence, head).
-  while ((max_keys + kps - 1) / kps > kCombineFanIn * kCombineFanIn) kps += chunk;
+  const long per = (total_rows + target - 1) / target;
+  long kps = ((per + chunk - 1) / chunk) * chunk;
+  if (kps < chunk) kps = chunk;
+  // Bound the partials the combine kernel reads per output.
+  while ((max_keys + kps - 1) / kps > kMaxDecodeSplits) kps += chunk;
   return (int)kps;
 }
 
-hipError_t launch_decode(hipStream_t st, const DecodeArgs &a, int D, int RB, int max_splits) {
+hipError_t launch_decode(hipStream_t st, const DecodeArgs &a, int D, int RB) {
   switch (D) {
-    case 64: return launch_d<64>(st, a, RB, max_splits);
-    case 128: return launch_d<128>(st, a, RB, max_splits);
-    case 256: return launch_d<256>(st, a, RB, max_splits);
+    case 64: return launch_d<64>(st, a, RB);
+    case 128: return launch_d<128>(st, a, RB);
+    case 256: return launch_d<256>(st, a, RB);
     default: return hipErrorInvalidValue;
   }
 }

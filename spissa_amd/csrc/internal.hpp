@@ -18,8 +18,8 @@ enum : int { kDevErrSoftmaxDenominator = 1 };
 
 // Largest batch a single decode launch carries in its kernel arguments.
 constexpr int kMaxDecodeBatch = 16;
-// Fan-in of the split-K combine tree.
-constexpr int kCombineFanIn = 16;
+// Most key splits of one (sequence, KV head) the decode combine reads.
+constexpr int kMaxDecodeSplits = 512;
 
 struct SeqDesc {
   const float *k;  // cache keys   [max_seq, Hkv, D] (may be null when past == 0)
@@ -29,19 +29,30 @@ struct SeqDesc {
 };
 
 struct DecodeArgs {
-  const float *q;      // [B, Hq, D]
-  const float *cur_k;  // [B, Hkv, D]: the new token's key
-  const float *cur_v;
+  float *q;            // [B, Hq, D]; rotated in place when rope_cos is set
+  float *cur_k;        // [B, Hkv, D]: the new token's key; rotated in place with q
+  const float *cur_v;  // [B, Hkv, D]
   float *out;          // [B, Hq, D]
-  float *partial;      // combine-tree entries
-  int *counters;       // combine-tree arrival counters (zero between launches)
+  float *partial;      // [B, Hkv, HB, max_splits] entries of RB*(D+2) floats
   int *err;            // device error bits
+  // Fused RoPE (rotate-half over the whole head, D/2 pairs): table rows are
+  // absolute positions; the new token of sequence b sits at position seq[b].past.
+  const float *rope_cos;  // [positions, D/2] or null (no RoPE)
+  const float *rope_sin;
+  // Fused append: cache rows seq[b].past receive the (rotated) new key and value.
+  float *app_k[kMaxDecodeBatch];
+  float *app_v[kMaxDecodeBatch];
+  // bf16 prefill shadow of the cache (null when the cache has none): the
+  // appended row also goes to kb [Hkv, cap, D] and vt [Hkv, D, cap].
+  bf16 *app_kb[kMaxDecodeBatch];
+  bf16 *app_vt[kMaxDecodeBatch];
+  long app_cap[kMaxDecodeBatch];
+  int do_append;
   int B, Hq, Hkv, R, HB;  // R = Hq/Hkv, HB = head blocks per kv head
   int window;
-  int kps;             // keys per split
-  int max_entries;     // combine-tree entries per (b, h, hb) for the largest split count
-  int max_counters;    // combine-tree counters per (b, h, hb)
-  float qscale;        // softmax scale * log2(e), folded into q
+  int kps;             // cached keys per split
+  int max_splits;      // splits of the longest sequence in the launch
+  float qscale;        // softmax scale * log2(e), applied to the scores
   SeqDesc seq[kMaxDecodeBatch];
 };
 
@@ -85,15 +96,13 @@ hipError_t launch_gemma_prologue(hipStream_t st, const float *cos_tab, const flo
 hipError_t launch_stage_bf16(hipStream_t st, const float *k_rows, const float *v_rows, size_t n,
                              size_t n_pad, size_t H, size_t D, bf16 *kb, bf16 *vt,
                              size_t dst_first, size_t dst_cap);
-hipError_t launch_decode(hipStream_t st, const DecodeArgs &a, int D, int RB, int max_splits);
+hipError_t launch_decode(hipStream_t st, const DecodeArgs &a, int D, int RB);
 hipError_t launch_prefill(hipStream_t st, const PrefillArgs &a, int D);
 hipError_t launch_generic(hipStream_t st, const GenericArgs &a);
 
-// Keys per split chosen for a decode launch.
-int decode_keys_per_split(int D, int RB, long total_keys_times_heads, int max_keys);
-// Entries / counters of the combine tree for nsplit leaves.
-int combine_tree_entries(int nsplit);
-int combine_tree_counters(int nsplit);
+// Keys per split of a decode launch: total_rows = key rows summed over all
+// (sequence, KV head, head block) triples; max_keys = longest visible range.
+int decode_keys_per_split(int D, int RB, long total_rows, int max_keys);
 bool decode_supported(int D, int R);
 bool prefill_supported(int D);
 

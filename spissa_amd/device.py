@@ -148,5 +148,19 @@ class Session:
             self.handle, _dev(q, "q"), _dev(k, "k"), _dev(v, "v"), arr, len(caches), C.byref(cfg),
             _dev(out, "out")))
 
+    def decode_step(self, table: Optional[RopeTable], q, k, v, caches: Sequence[KvCache],
+                    config: KvAttentionConfig, out) -> None:
+        """Fused RoPE + single-token attention + append for `len(caches)` sequences.
+
+        q [B, Hq, D], k/v [B, Hkv, D] are read-only; every cache gains one token
+        holding the rotated key and the value."""
+        arr = (_ffi.c_void_p * max(1, len(caches)))()
+        for i, c in enumerate(caches):
+            arr[i] = c.handle.value
+        cfg = config._c()
+        check(self._lib.spissa_decode_step_device(
+            self.handle, None if table is None else table.handle, _dev(q, "q"), _dev(k, "k"),
+            _dev(v, "v"), arr, len(caches), C.byref(cfg), _dev(out, "out")))
+
     def append(self, cache: KvCache, k, v, token_count: int) -> None:
         cache.append_device(_dev(k, "k"), _dev(v, "v"), token_count)

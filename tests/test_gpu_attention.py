@@ -175,3 +175,101 @@ def test_batched_decode_matches_per_sequence_oracle(gpu):
     got = out.cpu().numpy().reshape(B, -1)
     for b in range(B):
         assert rel_err(got[b], refs[b]) <= DECODE_TOL, b
+
+
+@pytest.mark.parametrize("kind,Hq,Hkv,D,P,window,base,div", [
+    ("llama-3B", 24, 8, 128, 2000, 0, 500000.0, 1.0),
+    ("llama-1B", 32, 8, 64, 511, 0, 500000.0, 1.0),
+    ("gemma-1B global", 4, 1, 256, 700, 0, 1e6, 8.0),
+    ("gemma-4B local", 8, 4, 256, 1500, 1024, 10000.0, 1.0),
+    ("first token", 24, 8, 128, 0, 0, 500000.0, 1.0),
+])
+def test_fused_decode_step_matches_rope_sdpa_append(gpu, kind, Hq, Hkv, D, P, window, base, div):
+    import torch
+
+    from spissa_amd import _ffi
+    from spissa_amd.device import Session
+
+    print(f"[case] fused decode {kind} P={P}", flush=True)
+    steps = 3
+    s = Session(0)
+    gemma = kind.startswith("gemma")
+    table = s.rope_table(_ffi.ROPE_GEMMA if gemma else _ffi.ROPE_LLAMA, D, base, div, max_positions=P + steps + 8)
+    cache = s.kv_cache(Hkv, D, P + steps)
+    ref = o.KvCache(Hkv, D, P + steps)
+    _, _, _, pk, pv = layer_inputs(20, 1, 1, P, Hq, Hkv, D)
+    if P:
+        cache.append(pk, pv, P)
+        ref.append(pk, pv, P)
+    cfg = gpu.KvAttentionConfig(1, Hq, Hkv, D, True, window)
+    for t in range(steps):
+        q, k, v, _, _ = layer_inputs(21, t, 1, 0, Hq, Hkv, D)
+        rq, rk = q.copy(), k.copy()
+        if gemma:
+            o.apply_gemma_rotary_inplace(rq, rk, Hq, Hkv, 1, D, D, base, P + t, div)
+        else:
+            o.apply_llama_rotary_inplace(rq, rk, Hq, Hkv, 1, D, D, base, P + t)
+        want = o.sdpa_with_cache(rq, rk, v, ref, 1, Hq, Hkv, D, True, window)
+        ref.append(rk, v, 1)
+        dq, dk, dv = (torch.from_numpy(x).cuda() for x in (q, k, v))
+        out = torch.empty_like(dq)
+        s.decode_step(table, dq, dk, dv, [cache], cfg, out)
+        s.sync()
+        assert rel_err(out.cpu().numpy(), want) <= DECODE_TOL
+        assert cache.len() == P + t + 1
+        assert np.array_equal(dq.cpu().numpy(), q) and np.array_equal(dk.cpu().numpy(), k), "inputs are read-only"
+    from tests.helpers import assert_bitwise
+    assert_bitwise(cache.keys(), ref.keys(), "keys after fused appends")
+    assert_bitwise(cache.values(), ref.values(), "values after fused appends")
+    with pytest.raises(gpu.ShapeError):  # full cache: validated before launching, nothing mutated
+        s.decode_step(table, dq, dk, dv, [cache], cfg, out)
+    assert cache.len() == P + steps
+
+
+def test_fused_decode_batch_after_prefill_keeps_shadow_consistent(gpu):
+    import torch
+
+    from spissa_amd import _ffi
+    from spissa_amd.device import Session
+
+    B, Hq, Hkv, D, S0 = 4, 8, 2, 128, 300
+    s = Session(0)
+    table = s.rope_table(_ffi.ROPE_LLAMA, D, 500000.0, max_positions=1024)
+    caches, refs = [], []
+    for b in range(B):
+        q, k, v, _, _ = layer_inputs(22, 0, S0 + 7 * b, 0, Hq, Hkv, D, sequence=b)
+        c, rc = s.kv_cache(Hkv, D, 512), o.KvCache(Hkv, D, 512)
+        n = S0 + 7 * b
+        dq, dk, dv = (torch.from_numpy(x).cuda() for x in (q, k, v))
+        dout = torch.empty_like(dq)
+        s.attention(dq, dk, dv, c, gpu.KvAttentionConfig(n, Hq, Hkv, D, True), dout)  # builds no shadow (P=0)
+        c.append(k, v, n)
+        rc.append(k, v, n)
+        caches.append(c), refs.append(rc)
+    # a chunked prefill on cache 0 creates its bf16 shadow
+    q, k, v, _, _ = layer_inputs(23, 0, 16, 0, Hq, Hkv, D)
+    got = gpu.scaled_dot_product_attention_with_cache(q, k, v, caches[0], gpu.KvAttentionConfig(16, Hq, Hkv, D, True))
+    assert rel_err(got, o.sdpa_with_cache(q, k, v, refs[0], 16, Hq, Hkv, D)) <= BF16_TOL
+    cfg = gpu.KvAttentionConfig(1, Hq, Hkv, D, True)
+    # 12 steps move cache 0 from 316 to 328 tokens, so the next chunk reads the
+    # shadow rows written by the fused appends (below the 8-aligned restaging tail).
+    for t in range(12):
+        qs, ks, vs, wants = [], [], [], []
+        for b in range(B):
+            q, k, v, _, _ = layer_inputs(24, t, 1, 0, Hq, Hkv, D, sequence=b)
+            rq, rk = q.copy(), k.copy()
+            o.apply_llama_rotary_inplace(rq, rk, Hq, Hkv, 1, D, D, 500000.0, refs[b].len())
+            wants.append(o.sdpa_with_cache(rq, rk, v, refs[b], 1, Hq, Hkv, D))
+            refs[b].append(rk, v, 1)
+            qs.append(q), ks.append(k), vs.append(v)
+        dq, dk, dv = (torch.from_numpy(np.concatenate(x)).cuda() for x in (qs, ks, vs))
+        out = torch.empty_like(dq)
+        s.decode_step(table, dq, dk, dv, caches, cfg, out)
+        s.sync()
+        got = out.cpu().numpy().reshape(B, -1)
+        for b in range(B):
+            assert rel_err(got[b], wants[b]) <= DECODE_TOL
+    # the shadow of cache 0 followed the fused appends: another chunk agrees with the oracle
+    q, k, v, _, _ = layer_inputs(25, 0, 9, 0, Hq, Hkv, D)
+    got = gpu.scaled_dot_product_attention_with_cache(q, k, v, caches[0], gpu.KvAttentionConfig(9, Hq, Hkv, D, True))
+    assert rel_err(got, o.sdpa_with_cache(q, k, v, refs[0], 9, Hq, Hkv, D)) <= BF16_TOL
