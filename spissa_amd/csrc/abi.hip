@@ -849,6 +849,11 @@ static int validate_attention(size_t q_len, size_t k_len, size_t v_len, const sp
   return SPISSA_OK;
 }
 
+// The split-K decode kernel addresses a cache buffer with 32-bit byte offsets.
+static bool decode_cache_fits(const spissa_kv_cache *c) {
+  return !c || (double)c->max_seq_len * c->width() * sizeof(float) < 4294967296.0;
+}
+
 static int pick_rb(int R) {
   if (R % 4 == 0) return 4;
   if (R % 3 == 0) return 3;
@@ -988,7 +993,7 @@ static int attention_device_impl(spissa_session *s, const float *d_q, const floa
   HIP_TRY(hipSetDevice(s->device));
   const int D = (int)c->head_dim;
   const int R = (int)(c->num_heads / c->kv_heads);
-  if (c->query_len == 1 && decode_supported(D, R))
+  if (c->query_len == 1 && decode_supported(D, R) && decode_cache_fits(cache))
     return run_decode(s, d_q, d_k, d_v, &cache, 1, c, d_out, nullptr, false);
   if (c->query_len > 1 && s->prefill_precision == SPISSA_PREFILL_BF16 && prefill_supported(D))
     return run_prefill(s, d_q, d_k, d_v, const_cast<spissa_kv_cache *>(cache), c, d_out);
@@ -1019,7 +1024,9 @@ extern "C" int spissa_attention_decode_batch_device(spissa_session *s, const flo
   HIP_TRY(hipSetDevice(s->device));
   const int D = (int)cfg->head_dim;
   const int R = (int)(cfg->num_heads / cfg->kv_heads);
-  if (decode_supported(D, R)) return run_decode(s, d_q, d_k, d_v, caches, batch, cfg, d_out, nullptr, false);
+  bool fits = true;
+  for (size_t b = 0; b < batch; ++b) fits = fits && decode_cache_fits(caches ? caches[b] : nullptr);
+  if (decode_supported(D, R) && fits) return run_decode(s, d_q, d_k, d_v, caches, batch, cfg, d_out, nullptr, false);
   for (size_t b = 0; b < batch; ++b) {
     const size_t qo = b * cfg->num_heads * cfg->head_dim, ko = b * cfg->kv_heads * cfg->head_dim;
     ST_TRY(run_generic(s, d_q + qo, d_k + ko, d_v + ko, caches ? caches[b] : nullptr, cfg, d_out + qo));
@@ -1041,6 +1048,8 @@ extern "C" int spissa_decode_step_device(spissa_session *s, const spissa_rope_ta
     ST_TRY(kv_validate_append(caches[b], 0, 0, 1, false, &n, &nl));
     if (caches[b]->session->device != s->device)
       return set_err(SPISSA_ERR_ARGUMENT, "cache %zu lives on another device", b);
+    if (!decode_cache_fits(caches[b]))
+      return set_err(SPISSA_ERR_SHAPE, "cache %zu exceeds the fused decode step's 4 GiB per-buffer limit", b);
   }
   const int D = (int)cfg->head_dim;
   if (!decode_supported(D, (int)(cfg->num_heads / cfg->kv_heads)))

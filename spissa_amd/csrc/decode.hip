@@ -41,35 +41,51 @@ __device__ __forceinline__ float dpp(float v) {
   return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xf, 0xf, false);
 }
 
-// Value of lane ^ 16 (v_permlane16_swap_b32) and of lane ^ 32 (v_permlane32_swap_b32).
-__device__ __forceinline__ float xor16(float v) {
-  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+// Source operand of a DPP add (all source lanes are valid for these controls,
+// so `old` is never read; 0 lets the compiler fold it into v_add_f32_dpp).
+template <int CTRL>
+__device__ __forceinline__ float dpp0(float v) {
+  return __builtin_amdgcn_update_dpp(0.0f, v, CTRL, 0xf, 0xf, false);
 }
-__device__ __forceinline__ float xor32(float v) {
-  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
-}
-// Value of lane ^ 8 (DPP row_ror:8 within each 16-lane row).
-__device__ __forceinline__ float xor8(float v) { return dpp<0x128>(v); }
 
-template <int M>
-__device__ __forceinline__ float lane_xor(float v) {
-  if constexpr (M == 8) return xor8(v);
-  else if constexpr (M == 16) return xor16(v);
-  else return xor32(v);
+// Sum / max of v with the value of lane ^ 16 or lane ^ 32 (one permlane swap).
+__device__ __forceinline__ float sum16(float v) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum32(float v) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float max16(float v) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max32(float v) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 // All-reduce (sum) over aligned groups of LPR lanes.
 template <int LPR>
 __device__ __forceinline__ float group_sum(float v) {
   static_assert(LPR >= 2 && LPR <= 64 && (LPR & (LPR - 1)) == 0, "LPR");
-  v += dpp<0xB1>(v);                           // lane ^ 1  (quad_perm [1,0,3,2])
-  if constexpr (LPR >= 4) v += dpp<0x4E>(v);   // lane ^ 2  (quad_perm [2,3,0,1])
-  if constexpr (LPR >= 8) v += dpp<0x141>(v);  // quad <-> quad (row_half_mirror)
-  if constexpr (LPR >= 16) v += dpp<0x140>(v); // 8 <-> 8 (row_mirror)
-  if constexpr (LPR >= 32) v += xor16(v);      // row <-> row
-  if constexpr (LPR >= 64) v += xor32(v);      // half <-> half
+  v += dpp0<0xB1>(v);                           // lane ^ 1  (quad_perm [1,0,3,2])
+  if constexpr (LPR >= 4) v += dpp0<0x4E>(v);   // lane ^ 2  (quad_perm [2,3,0,1])
+  if constexpr (LPR >= 8) v += dpp0<0x141>(v);  // quad <-> quad (row_half_mirror)
+  if constexpr (LPR >= 16) v += dpp0<0x140>(v); // 8 <-> 8 (row_mirror)
+  if constexpr (LPR >= 32) v = sum16(v);        // row <-> row
+  if constexpr (LPR >= 64) v = sum32(v);        // half <-> half
+  return v;
+}
+
+// Max over the row groups of a wave (lanes l, l ^ LPR, l ^ 2 LPR, ...), for a
+// value that is uniform within each group of LPR lanes.
+template <int LPR>
+__device__ __forceinline__ float groups_max(float v) {
+  if constexpr (LPR <= 8) v = fmaxf(v, __builtin_amdgcn_update_dpp(v, v, 0x128, 0xf, 0xf, false));  // row_ror:8
+  if constexpr (LPR <= 16) v = max16(v);
+  if constexpr (LPR <= 32) v = max32(v);
   return v;
 }
 
@@ -97,9 +113,6 @@ __device__ __forceinline__ float4 fma4(float p, float4 v, float4 acc) {
   return make_float4(fmaf(p, v.x, acc.x), fmaf(p, v.y, acc.y), fmaf(p, v.z, acc.z),
                      fmaf(p, v.w, acc.w));
 }
-__device__ __forceinline__ float4 axpby4(float4 x, float a, float4 y, float b) {
-  return make_float4(x.x * a + y.x * b, x.y * a + y.y * b, x.z * a + y.z * b, x.w * a + y.w * b);
-}
 
 constexpr float NEG_INF = -__builtin_inff();
 
@@ -115,28 +128,6 @@ __device__ __forceinline__ void rotate_pair(float &first, float &second, float c
   second = b;
 }
 
-// Merges the online-softmax state of this lane with lane ^ M (same dims, other row group).
-template <int RB, int M>
-__device__ __forceinline__ void merge_with(float (&m)[RB], float (&l)[RB], float4 (&o)[RB][2]) {
-#pragma unroll
-  for (int r = 0; r < RB; ++r) {
-    const float mp = lane_xor<M>(m[r]);
-    const float lp = lane_xor<M>(l[r]);
-    float4 op0, op1;
-    op0.x = lane_xor<M>(o[r][0].x); op0.y = lane_xor<M>(o[r][0].y);
-    op0.z = lane_xor<M>(o[r][0].z); op0.w = lane_xor<M>(o[r][0].w);
-    op1.x = lane_xor<M>(o[r][1].x); op1.y = lane_xor<M>(o[r][1].y);
-    op1.z = lane_xor<M>(o[r][1].z); op1.w = lane_xor<M>(o[r][1].w);
-    const float mn = fmaxf(m[r], mp);
-    const float ms = safe_max(mn);
-    const float fa = fast_exp2(m[r] - ms), fb = fast_exp2(mp - ms);
-    l[r] = l[r] * fa + lp * fb;
-    o[r][0] = axpby4(o[r][0], fa, op0, fb);
-    o[r][1] = axpby4(o[r][1], fa, op1, fb);
-    m[r] = mn;
-  }
-}
-
 }  // namespace
 
 // At least 4 waves per SIMD (<= 128 VGPRs): four workgroups per CU stay resident.
@@ -148,8 +139,9 @@ __global__ __launch_bounds__(256, 4) void decode_split_kernel(const DecodeArgs a
   constexpr int HALF = D / 2;
   constexpr int ENTRY = RB * (D + 2);  // O[RB][D] then (max, sum)[RB]
 
-  __shared__ float w_o[4][RB][D];
-  __shared__ float w_ml[4][RB][2];
+  __shared__ float red_o[NG][RB][D];
+  __shared__ float red_l[NG][RB];
+  __shared__ float wave_m[4][RB];
 
   // Head blocks are the fastest grid dimension: the workgroups that read the
   // same key rows (all KV heads of one split) are dispatched back to back.
@@ -171,9 +163,35 @@ __global__ __launch_bounds__(256, 4) void decode_split_kernel(const DecodeArgs a
   const int grp = wave * GPW + lane / LPR;
   const int qh0 = h * a.R + hb * RB;
 
-  const long row_stride = (long)a.Hkv * D;
-  const float *kcache = a.seq[b].k + (long)h * D;
-  const float *vcache = a.seq[b].v + (long)h * D;
+  // K/V rows are addressed as 32-bit byte offsets from the (uniform, SGPR)
+  // cache base -- the host keeps cache buffers under 4 GiB for this kernel --
+  // so a row costs one VGPR of address (shared by K and V) instead of four.
+  const unsigned row_bytes = (unsigned)(a.Hkv * D * 4);
+  const char *kcache = reinterpret_cast<const char *>(a.seq[b].k);
+  const char *vcache = reinterpret_cast<const char *>(a.seq[b].v);
+  const unsigned lane_off = (unsigned)((h * D + 4 * sub) * 4);
+
+  float4 kr[RPG][2], vr[RPG][2];
+  bool valid[RPG];
+  auto load_chunk = [&](int c) {
+#pragma unroll
+    for (int i = 0; i < RPG; ++i) {
+      const int j = c + grp + i * NG;
+      valid[i] = j < k1;
+      if (valid[i]) {
+        const unsigned off = (unsigned)j * row_bytes + lane_off;
+        kr[i][0] = *reinterpret_cast<const float4 *>(kcache + off);
+        kr[i][1] = *reinterpret_cast<const float4 *>(kcache + off + HALF * 4);
+        vr[i][0] = *reinterpret_cast<const float4 *>(vcache + off);
+        vr[i][1] = *reinterpret_cast<const float4 *>(vcache + off + HALF * 4);
+      } else {
+        kr[i][0] = kr[i][1] = vr[i][0] = vr[i][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+  };
+  // The first chunk's K/V loads go out before q and the RoPE table: the loads
+  // return in order, so q is ready when the K/V rows are, at no extra latency.
+  load_chunk(k0);
 
   float4 qv[RB][2];
   {
@@ -195,6 +213,8 @@ __global__ __launch_bounds__(256, 4) void decode_split_kernel(const DecodeArgs a
       }
     }
   }
+  // Online softmax with one running maximum per head shared by the whole wave
+  // (log2 domain), so the row groups' sums and outputs add without rescaling.
   float m[RB], l[RB];
   float4 o[RB][2];
 #pragma unroll
@@ -204,88 +224,69 @@ __global__ __launch_bounds__(256, 4) void decode_split_kernel(const DecodeArgs a
     o[r][0] = make_float4(0.f, 0.f, 0.f, 0.f);
     o[r][1] = o[r][0];
   }
+  const float qs = a.qscale;
 
   for (int c = k0; c < k1; c += NG * RPG) {
-    float4 kr[RPG][2], vr[RPG][2];
-    bool valid[RPG];
+    if (c != k0) load_chunk(c);
+    float d[RPG][RB];
 #pragma unroll
-    for (int i = 0; i < RPG; ++i) {
-      const int j = c + grp + i * NG;
-      valid[i] = j < k1;
-      if (valid[i]) {
-        const float *kp = kcache + (long)j * row_stride;
-        const float *vp = vcache + (long)j * row_stride;
-        kr[i][0] = ld4(kp + 4 * sub);
-        kr[i][1] = ld4(kp + HALF + 4 * sub);
-        vr[i][0] = ld4(vp + 4 * sub);
-        vr[i][1] = ld4(vp + HALF + 4 * sub);
-      } else {
-        kr[i][0] = kr[i][1] = vr[i][0] = vr[i][1] = make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-    }
-    float sc[RPG][RB];
+    for (int i = 0; i < RPG; ++i)
 #pragma unroll
-    for (int i = 0; i < RPG; ++i) {
-#pragma unroll
-      for (int r = 0; r < RB; ++r) {
-        const float s = group_sum<LPR>(dot8(qv[r][0], qv[r][1], kr[i][0], kr[i][1])) * a.qscale;
-        sc[i][r] = valid[i] ? s : NEG_INF;
-      }
-    }
+      for (int r = 0; r < RB; ++r) d[i][r] = group_sum<LPR>(dot8(qv[r][0], qv[r][1], kr[i][0], kr[i][1]));
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
-      float mx = m[r];
+      float cm = NEG_INF;
 #pragma unroll
-      for (int i = 0; i < RPG; ++i) mx = fmaxf(mx, sc[i][r]);
-      const float ms = safe_max(mx);
+      for (int i = 0; i < RPG; ++i) cm = valid[i] ? fmaxf(cm, d[i][r]) : cm;
+      cm = groups_max<LPR>(cm);
+      const float mnew = fmaxf(m[r], cm * qs);
+      const float ms = safe_max(mnew);
       const float alpha = fast_exp2(m[r] - ms);
       l[r] *= alpha;
       o[r][0] = scale4(o[r][0], alpha);
       o[r][1] = scale4(o[r][1], alpha);
 #pragma unroll
       for (int i = 0; i < RPG; ++i) {
-        const float p = fast_exp2(sc[i][r] - ms);
+        const float p = valid[i] ? fast_exp2(fmaf(d[i][r], qs, -ms)) : 0.0f;
         l[r] += p;
         o[r][0] = fma4(p, vr[i][0], o[r][0]);
         o[r][1] = fma4(p, vr[i][1], o[r][1]);
       }
-      m[r] = mx;
+      m[r] = mnew;
     }
   }
 
-  // ---- merge the row groups of each wave in registers ----
-  if constexpr (GPW >= 8) merge_with<RB, 8>(m, l, o);
-  if constexpr (GPW >= 4) merge_with<RB, 16>(m, l, o);
-  if constexpr (GPW >= 2) merge_with<RB, 32>(m, l, o);
-  // Lanes of row group 0 now hold the wave's state; merge the four waves in LDS.
-  if (lane < LPR) {
+  // ---- merge: the groups of a wave share m, the four waves are rescaled ----
 #pragma unroll
-    for (int r = 0; r < RB; ++r) {
-      *reinterpret_cast<float4 *>(&w_o[wave][r][4 * sub]) = o[r][0];
-      *reinterpret_cast<float4 *>(&w_o[wave][r][HALF + 4 * sub]) = o[r][1];
-      if (sub == 0) {
-        w_ml[wave][r][0] = m[r];
-        w_ml[wave][r][1] = l[r];
-      }
-    }
+  for (int r = 0; r < RB; ++r) {
+    *reinterpret_cast<float4 *>(&red_o[grp][r][4 * sub]) = o[r][0];
+    *reinterpret_cast<float4 *>(&red_o[grp][r][HALF + 4 * sub]) = o[r][1];
+    if (sub == 0) red_l[grp][r] = l[r];
+    if (lane == 0) wave_m[wave][r] = m[r];
   }
   __syncthreads();
 
   const long bhh = ((long)b * a.Hkv + h) * a.HB + hb;
   float *dst = a.partial + (bhh * a.max_splits + split) * (long)ENTRY;
   for (int e = tid; e < RB * D; e += 256) {
-    const int r = e / D;
-    const float M = fmaxf(fmaxf(w_ml[0][r][0], w_ml[1][r][0]), fmaxf(w_ml[2][r][0], w_ml[3][r][0]));
+    const int r = e / D, dim = e % D;
+    const float M = fmaxf(fmaxf(wave_m[0][r], wave_m[1][r]), fmaxf(wave_m[2][r], wave_m[3][r]));
     const float Ms = safe_max(M);
-    float L = 0.0f, O = 0.0f;
+    float O = 0.0f, L = 0.0f;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      const float f = fast_exp2(w_ml[w][r][0] - Ms);
-      L += w_ml[w][r][1] * f;
-      O += w_o[w][r][e % D] * f;
+      float ow = 0.0f, lw = 0.0f;
+#pragma unroll
+      for (int g = 0; g < GPW; ++g) {
+        ow += red_o[w * GPW + g][r][dim];
+        lw += red_l[w * GPW + g][r];
+      }
+      const float f = fast_exp2(wave_m[w][r] - Ms);
+      O = fmaf(ow, f, O);
+      L = fmaf(lw, f, L);
     }
     dst[e] = O;
-    if ((e % D) == 0) {
+    if (dim == 0) {
       dst[RB * D + 2 * r] = M;
       dst[RB * D + 2 * r + 1] = L;
     }
@@ -323,33 +324,11 @@ __global__ __launch_bounds__(1024) void decode_combine_kernel(const DecodeArgs a
   const float *knew = a.cur_k + ((long)b * a.Hkv + h) * D;
   const float *vnew = a.cur_v + ((long)b * a.Hkv + h) * D;
 
-  // ---- the new token: (rotated) q . (rotated) k for the RB query heads ----
-  float kd = 0.0f;  // this thread's (rotated) key element, kept for the append
-  if (tid < RB * D) {
-    const int rr = tid / D, d = tid % D;
-    const float *qrow = a.q + ((long)b * a.Hq + qh0 + rr) * D;
-    float qd = qrow[d];
-    kd = knew[d];
-    if (a.rope_cos) {
-      const int pair = d % HALF;
-      const float c = a.rope_cos[(long)P * HALF + pair], sn = a.rope_sin[(long)P * HALF + pair];
-      float q1 = qrow[pair], q2 = qrow[pair + HALF], k1 = knew[pair], k2 = knew[pair + HALF];
-      rotate_pair(q1, q2, c, sn);
-      rotate_pair(k1, k2, c, sn);
-      qd = d < HALF ? q1 : q2;
-      kd = d < HALF ? k1 : k2;
-    }
-    float prod = qd * kd;
-    prod = group_sum<64>(prod);
-    if ((tid & 63) == 0) s_dot[tid >> 6] = prod;
-  }
-
-  // ---- the cached keys: partials of the splits ----
+  // ---- loads first: the first batch of split partials, then the new token ----
   const long bhh = ((long)b * a.Hkv + h) * a.HB + hb;
   const float *ents = a.partial + bhh * a.max_splits * (long)ENTRY;
-  float m = NEG_INF, l = 0.0f, o = 0.0f;
-  for (int s0 = sl; s0 < nsplit; s0 += SL * UNROLL) {
-    float ms[UNROLL], ls[UNROLL], os[UNROLL];
+  float ms[UNROLL], ls[UNROLL], os[UNROLL];
+  auto load_batch = [&](int s0) {
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
       const int s = s0 + u * SL;
@@ -364,6 +343,33 @@ __global__ __launch_bounds__(1024) void decode_combine_kernel(const DecodeArgs a
         os[u] = 0.0f;
       }
     }
+  };
+  load_batch(sl);
+
+  float kd = 0.0f;  // this thread's (rotated) key element, kept for the append
+  float prod = 0.0f;
+  if (tid < RB * D) {
+    const int rr = tid / D, d = tid % D;
+    const float *qrow = a.q + ((long)b * a.Hq + qh0 + rr) * D;
+    float qd = qrow[d];
+    kd = knew[d];
+    if (a.rope_cos) {
+      const int pair = d % HALF;
+      const float c = a.rope_cos[(long)P * HALF + pair], sn = a.rope_sin[(long)P * HALF + pair];
+      float q1 = qrow[pair], q2 = qrow[pair + HALF], k1 = knew[pair], k2 = knew[pair + HALF];
+      rotate_pair(q1, q2, c, sn);
+      rotate_pair(k1, k2, c, sn);
+      qd = d < HALF ? q1 : q2;
+      kd = d < HALF ? k1 : k2;
+    }
+    prod = qd * kd;
+  }
+  const float vd_out = vnew[e % D];
+
+  // ---- merge the splits ----
+  float m = NEG_INF, l = 0.0f, o = 0.0f;
+  for (int s0 = sl; s0 < nsplit; s0 += SL * UNROLL) {
+    if (s0 != sl) load_batch(s0);
     float mx = m;
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) mx = fmaxf(mx, ms[u]);
@@ -378,6 +384,12 @@ __global__ __launch_bounds__(1024) void decode_combine_kernel(const DecodeArgs a
       o += os[u] * g;
     }
     m = mx;
+  }
+
+  // ---- the new token's score: q . k over the head, per query head ----
+  if (tid < RB * D) {
+    prod = group_sum<64>(prod);
+    if ((tid & 63) == 0) s_dot[tid >> 6] = prod;
   }
   s_m[sl][out] = m;
   s_l[sl][out] = l;
@@ -397,7 +409,7 @@ __global__ __launch_bounds__(1024) void decode_combine_kernel(const DecodeArgs a
     for (int k = 0; k < SL; ++k) M = fmaxf(M, s_m[k][out]);
     const float Ms = safe_max(M);
     const float pn = fast_exp2(sn - Ms);
-    float L = pn, O = pn * vnew[e % D];
+    float L = pn, O = pn * vd_out;
 #pragma unroll
     for (int k = 0; k < SL; ++k) {
       const float g = fast_exp2(s_m[k][out] - Ms);
@@ -421,9 +433,10 @@ __global__ __launch_bounds__(1024) void decode_combine_kernel(const DecodeArgs a
 }
 
 namespace {
-// Rows per lane group in flight: four, three for four query heads per block
-// (keeps the split kernel within 128 VGPRs without spills).
-constexpr int rows_per_group(int RB) { return RB >= 4 ? 3 : 4; }
+// Rows per lane group in flight: three (two for four query heads per block)
+// keep the split kernel within 128 VGPRs without spills, so four workgroups
+// stay resident per CU.
+constexpr int rows_per_group(int RB) { return RB >= 4 ? 2 : 3; }
 
 template <int D, int RB>
 hipError_t launch_one(hipStream_t st, const DecodeArgs &a) {
