@@ -99,10 +99,9 @@ def gpu_bench(args) -> dict:
         cfg1 = KvAttentionConfig(1, HQ, HKV, D, True)
 
         def decode_step():
+            # rope(q, k) -> attention -> append(k, v) per layer, fused in two launches
             for l in range(LAYERS):
-                sess.rope_apply(table, qs[l], ks[l], 1, HQ, HKV, D, CTX)
-                sess.attention(qs[l], ks[l], vs[l], caches[l], cfg1, outs[l])
-                sess.append(caches[l], ks[l], vs[l], 1)
+                sess.decode_step(table, qs[l], ks[l], vs[l], [caches[l]], cfg1, outs[l])
 
         def reset_lengths():
             for c in caches:
@@ -172,13 +171,20 @@ def gpu_bench(args) -> dict:
 
             def batch_step():
                 for l in range(LAYERS):
-                    sess.attention_decode_batch(bq[l], bk[l], bv[l], bcaches[l], cfg1, bo[l])
+                    sess.decode_step(table, bq[l], bk[l], bv[l], bcaches[l], cfg1, bo[l])
+
+            def reset_batch():
+                for row in bcaches:
+                    for c in row:
+                        c.truncate(CTX)
 
             batch_step()
             sess.sync()
+            reset_batch()
             g_b = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g_b, stream=stream):
                 batch_step()
+            reset_batch()
             ms_b = time_graph(g_b, max(3, args.steps // 2), 2)
             res["decode_b16"] = {
                 "ms_per_step": ms_b,
@@ -313,7 +319,7 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic (torch.randn N(0,1) K/V/Q resident in HBM)",
         "config": {"workload": "llama-3.2-3B attention decode, 8192-token KV cache, batch 1, 28 layers "
-                               "(RoPE + split-K decode + KV append per layer)",
+                               "(RoPE + split-K decode + KV append per layer, fused in two launches)",
                    "heads": f"{HQ}q/{HKV}kv", "head_dim": D, "context": CTX, "layers": LAYERS},
         "us_per_layer": round(d1["us_per_layer"], 3),
         "decode_b1": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in d1.items()},
@@ -324,7 +330,8 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(d1["attn_kernel_GBps"] / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": "decode_kernel<128,3,4> (split-K f32 decode), avg of 28 back-to-back launches per replay",
+            "kernel": "one decode attention launch = decode_split_kernel<128,3,3> + decode_combine_kernel<128,3>; "
+                      "event-timed average over 28 back-to-back launches per graph replay",
         },
         "hbm_read_probe_GBps": res.get("hbm_read_probe_GBps"),
         "device": res.get("device"),

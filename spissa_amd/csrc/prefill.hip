@@ -47,7 +47,7 @@ __device__ __forceinline__ bf16x8 cat(bf16x4 a, bf16x4 b) {
 }  // namespace
 
 template <int D, int RB, int NPB, int BN>
-__global__ __launch_bounds__(RB *NPB * 64) void prefill_kernel(const PrefillArgs a) {
+__global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillArgs a) {
   constexpr int NW = RB * NPB;
   constexpr int NT = NW * 64;
   constexpr int KS = D + 8;   // K tile row stride (bf16), padded against LDS bank conflicts
@@ -105,7 +105,10 @@ __global__ __launch_bounds__(RB *NPB * 64) void prefill_kernel(const PrefillArgs
   for (int d = 0; d < DB; ++d)
 #pragma unroll
     for (int i = 0; i < 16; ++i) oacc[d][i] = 0.0f;
+  // Running max m is kept in the scaled log2 domain; scores stay raw and the
+  // scale is folded into the exp2 argument.
   float m = NEG_INF, l = 0.0f;
+  const float c = a.qk_scale_log2;
 
   const int wave_min_q = a.P + wp0;
   const int wave_max_q = a.P + min(wp0 + 31, a.S - 1);
@@ -115,16 +118,16 @@ __global__ __launch_bounds__(RB *NPB * 64) void prefill_kernel(const PrefillArgs
     const int kt0 = t * BN;
     __syncthreads();
     // ---- stage the K tile [BN][D] and the V^T tile [D][BN] in LDS ----
-    for (int c = threadIdx.x; c < BN * (D / 8); c += NT) {
-      const int row = c / (D / 8), col = (c % (D / 8)) * 8;
+    for (int cc = threadIdx.x; cc < BN * (D / 8); cc += NT) {
+      const int row = cc / (D / 8), col = (cc % (D / 8)) * 8;
       const int key = kt0 + row;
       const bf16 *src = key < a.P8
                             ? a.kb_cache + ((long)h * a.cap_cache + key) * D
                             : a.kb_stage + ((long)h * a.cap_stage + (key - a.P8)) * D;
       *reinterpret_cast<uint4 *>(&Ks[row * KS + col]) = *reinterpret_cast<const uint4 *>(src + col);
     }
-    for (int c = threadIdx.x; c < D * (BN / 8); c += NT) {
-      const int dim = c / (BN / 8), kc = (c % (BN / 8)) * 8;
+    for (int cc = threadIdx.x; cc < D * (BN / 8); cc += NT) {
+      const int dim = cc / (BN / 8), kc = (cc % (BN / 8)) * 8;
       const int key = kt0 + kc;
       const bf16 *src = key < a.P8
                             ? a.vt_cache + ((long)h * D + dim) * a.cap_cache + key
@@ -139,7 +142,7 @@ __global__ __launch_bounds__(RB *NPB * 64) void prefill_kernel(const PrefillArgs
                         !(a.window > 0 && kt0 + BN - 1 + a.window <= wave_min_q);
     if (!active) continue;
 
-    // ---- S^T = K Q^T ----
+    // ---- S^T = K Q^T (raw scores) ----
     f32x16 sacc[KB];
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
@@ -153,49 +156,63 @@ __global__ __launch_bounds__(RB *NPB * 64) void prefill_kernel(const PrefillArgs
       }
     }
 
-    // ---- mask, scale, online softmax ----
+    // ---- mask (diagonal and tail tiles only), tile max ----
     const bool need_mask = (a.causal && kt0 + BN - 1 > wave_min_q) ||
                            (a.window > 0 && kt0 + a.window <= wave_max_q) ||
                            (kt0 + BN > key_total);
-    float tmax = NEG_INF;
+    // The masked scores go to a copy: writing -inf in place into the MFMA
+    // accumulator registers gave wrong results on masked tiles.
+    float sc[KB][16];
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) {
+    for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float s = sacc[kb][i] * a.qk_scale_log2;
-        if (need_mask) {
+      for (int i = 0; i < 16; ++i) sc[kb][i] = sacc[kb][i];
+    if (need_mask) {
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
           const int key = kt0 + kb * 32 + 8 * (i >> 2) + 4 * hl + (i & 3);
           const bool masked = (a.causal && key > q_abs) ||
                               (a.window > 0 && key + a.window <= q_abs) || key >= key_total;
-          if (masked) s = NEG_INF;
+          if (masked) sc[kb][i] = NEG_INF;
         }
-        sacc[kb][i] = s;
-        tmax = fmaxf(tmax, s);
       }
     }
-    tmax = xor32_max(tmax);
+    float tmax = NEG_INF;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; i += 2) tmax = fmaxf(tmax, fmaxf(sc[kb][i], sc[kb][i + 1]));
+    tmax = xor32_max(tmax) * c;
+
+    // ---- online softmax; rescale O only when some row's maximum grew ----
     const float mnew = fmaxf(m, tmax);
     const float ms = mnew == NEG_INF ? 0.0f : mnew;
-    const float alpha = fast_exp2(m - ms);
+    if (__ballot(mnew > m)) {
+      const float alpha = fast_exp2(m - ms);
+      l *= alpha;
+#pragma unroll
+      for (int d = 0; d < DB; ++d)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) oacc[d][i] *= alpha;
+    }
     m = mnew;
-    l *= alpha;
-#pragma unroll
-    for (int d = 0; d < DB; ++d)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) oacc[d][i] *= alpha;
 
     // ---- O^T += V^T P^T ----
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
       bf16x8 pa, pb;
+      float ls = 0.0f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float p0v = fast_exp2(sacc[kb][i] - ms);
-        const float p1v = fast_exp2(sacc[kb][i + 8] - ms);
-        l += p0v + p1v;
+        const float p0v = fast_exp2(fmaf(sc[kb][i], c, -ms));
+        const float p1v = fast_exp2(fmaf(sc[kb][i + 8], c, -ms));
+        ls += p0v + p1v;
         pa[i] = (bf16)p0v;
         pb[i] = (bf16)p1v;
       }
+      l += ls;
 #pragma unroll
       for (int d = 0; d < DB; ++d) {
         const bf16 *vrow = &Vs[(d * 32 + lq) * VS + kb * 32 + 4 * hl];
@@ -240,10 +257,12 @@ hipError_t launch_cfg(hipStream_t st, PrefillArgs a) {
   return hipGetLastError();
 }
 
+// Four waves per workgroup (one per SIMD): four query heads of a KV group
+// with one 32-position block, two heads with two blocks, or one head with four
+// blocks (also for groups of three or five heads).
 template <int D>
 hipError_t launch_d(hipStream_t st, const PrefillArgs &a) {
   if (a.R % 4 == 0) return launch_cfg<D, 4, 1>(st, a);
-  if (a.R % 3 == 0) return launch_cfg<D, 3, 1>(st, a);
   if (a.R % 2 == 0) return launch_cfg<D, 2, 2>(st, a);
   return launch_cfg<D, 1, 4>(st, a);
 }
