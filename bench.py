@@ -150,6 +150,15 @@ def gpu_bench(args) -> dict:
         }
         del g_step, g_attn
 
+        if args.copy_probe:
+            # A plain copy of known size: 256 MiB read + 256 MiB written per launch.
+            src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
+            dst = torch.empty_like(src)
+            for _ in range(3):
+                dst.copy_(src)
+            torch.cuda.synchronize()
+            del src, dst
+
         # ---- decode, batch 16 ----
         if not args.decode_only:
             log("filling batch-16 caches")
@@ -294,6 +303,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-only", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run a 256 MiB device copy (HBM-counter calibration under rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build's attention path has no multi-GPU leg "

@@ -952,14 +952,16 @@ static int run_prefill(spissa_session *s, const float *d_q, const float *d_k, co
   const int D = (int)c->head_dim, Hkv = (int)c->kv_heads;
   const int P = cache ? (int)cache->len : 0;
   const int S = (int)c->query_len;
-  const int P8 = P & ~7;
+  // Keys [0, P8) are read from the cache's bf16 shadow, keys [P8, P+S) from
+  // the staging buffer; P8 is tile-aligned so no key tile straddles the two.
+  const int P8 = P & ~(kPrefillTileAlign - 1);
   if (cache && P8 > 0) ST_TRY(ensure_shadow(cache, s->stream));
-  const size_t cap_stage = (((size_t)P + S + 63) & ~(size_t)63) - P8;
+  const size_t cap_stage = (((size_t)P + S + kPrefillTileAlign - 1) & ~(size_t)(kPrefillTileAlign - 1)) - P8;
   ST_TRY(ensure_buf(s, s->stage, 2 * (size_t)Hkv * cap_stage * D * sizeof(bf16), false));
   bf16 *kb_stage = (bf16 *)s->stage.p;
   bf16 *vt_stage = kb_stage + (size_t)Hkv * cap_stage * D;
   const size_t w = (size_t)Hkv * D;
-  const int tail = P - P8;  // cached rows re-staged so the staging buffer starts 8-aligned
+  const int tail = P - P8;  // cached rows re-staged so the staging buffer starts tile-aligned
   if (tail > 0)
     HIP_TRY(launch_stage_bf16(s->stream, cache->keys + (size_t)P8 * w, cache->values + (size_t)P8 * w, tail, tail,
                               Hkv, D, kb_stage, vt_stage, 0, cap_stage));

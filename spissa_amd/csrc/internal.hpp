@@ -20,6 +20,9 @@ enum : int { kDevErrSoftmaxDenominator = 1 };
 constexpr int kMaxDecodeBatch = 16;
 // Most key splits of one (sequence, KV head) the decode combine reads.
 constexpr int kMaxDecodeSplits = 512;
+// Prefill key tiles are at most this wide; the staging buffer starts at a
+// multiple of it.
+constexpr int kPrefillTileAlign = 64;
 
 struct SeqDesc {
   const float *k;  // cache keys   [max_seq, Hkv, D] (may be null when past == 0)
@@ -59,7 +62,9 @@ struct DecodeArgs {
 struct PrefillArgs {
   const float *q;     // [S, Hq, D] f32
   float *out;         // [S, Hq, D] f32
-  // bf16 K/V for keys [0, P8) come from the cache shadow, keys [P8, P+S) from the staging buffer.
+  // bf16 K/V for keys [0, P8) come from the cache shadow, keys [P8, P+S) from
+  // the staging buffer; P8 is a multiple of kPrefillTileAlign, so no key tile
+  // straddles the two.
   const bf16 *kb_cache;  // [Hkv, cap_cache, D]
   const bf16 *vt_cache;  // [Hkv, D, cap_cache]
   const bf16 *kb_stage;  // [Hkv, cap_stage, D], key 0 of the buffer is absolute key P8

@@ -28,6 +28,8 @@ namespace {
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
 typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(4))) unsigned u32x4;
+typedef __attribute__((ext_vector_type(2))) unsigned u32x2;
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -40,14 +42,19 @@ __device__ __forceinline__ float xor32_sum(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+__device__ __forceinline__ u32x2 kreg_lo(u32x4 v) { return __builtin_shufflevector(v, v, 0, 1); }
+__device__ __forceinline__ u32x2 kreg_hi(u32x4 v) { return __builtin_shufflevector(v, v, 2, 3); }
+
 __device__ __forceinline__ bf16x8 cat(bf16x4 a, bf16x4 b) {
   return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
 }  // namespace
 
+// Two waves per SIMD up to head_dim 128; head_dim 256 (O alone is 128
+// accumulators per lane) takes one wave per SIMD with the full register file.
 template <int D, int RB, int NPB, int BN>
-__global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillArgs a) {
+__global__ __launch_bounds__(RB *NPB * 64, D >= 256 ? 1 : 2) void prefill_kernel(const PrefillArgs a) {
   constexpr int NW = RB * NPB;
   constexpr int NT = NW * 64;
   constexpr int KS = D + 8;   // K tile row stride (bf16), padded against LDS bank conflicts
@@ -114,29 +121,64 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
   const int wave_max_q = a.P + min(wp0 + 31, a.S - 1);
   const bool wave_live = wp0 < a.S;
 
-  for (int t = t_begin; t < t_end; ++t) {
+  // Per-thread staging slots, fixed for the whole loop: K chunk (row, 8 dims)
+  // and V^T chunk (dim, 8 keys) offsets inside a tile and inside LDS.
+  constexpr int KCH = BN * (D / 8) / NT;  // 16-byte K chunks per thread per tile
+  constexpr int VCH = D * (BN / 8) / NT;  // 16-byte V^T chunks per thread per tile
+  static_assert(KCH * NT == BN * (D / 8) && VCH * NT == D * (BN / 8), "tile/thread mismatch");
+  int k_row[KCH], k_lds[KCH], v_dim[VCH], v_kc[VCH], v_lds[VCH];
+#pragma unroll
+  for (int u = 0; u < KCH; ++u) {
+    const int cc = threadIdx.x + u * NT;
+    k_row[u] = cc / (D / 8);
+    const int col = (cc % (D / 8)) * 8;
+    k_lds[u] = k_row[u] * KS + col;
+    k_row[u] = k_row[u] * D + col;  // element offset of the chunk inside a tile of D-wide rows
+  }
+#pragma unroll
+  for (int u = 0; u < VCH; ++u) {
+    const int cc = threadIdx.x + u * NT;
+    v_dim[u] = cc / (BN / 8);
+    v_kc[u] = (cc % (BN / 8)) * 8;
+    v_lds[u] = v_dim[u] * VS + v_kc[u];
+  }
+  const bf16 *kb_c = a.kb_cache + (long)h * a.cap_cache * D;
+  const bf16 *kb_s = a.kb_stage + (long)h * a.cap_stage * D;
+  const bf16 *vt_c = a.vt_cache + (long)h * D * a.cap_cache;
+  const bf16 *vt_s = a.vt_stage + (long)h * D * a.cap_stage;
+
+  // The next tile's K / V^T chunks are loaded into registers while the
+  // current tile is computed (register double buffering). Tiles never straddle
+  // the cache / staging boundary P8 (a multiple of the tile width), so the
+  // source buffer is a uniform choice per tile. Iteration t_begin - 1 only
+  // loads the first tile.
+  u32x4 kreg[KCH], vreg[VCH];
+  for (int t = t_begin - 1; t < t_end; ++t) {
     const int kt0 = t * BN;
-    __syncthreads();
-    // ---- stage the K tile [BN][D] and the V^T tile [D][BN] in LDS ----
-    for (int cc = threadIdx.x; cc < BN * (D / 8); cc += NT) {
-      const int row = cc / (D / 8), col = (cc % (D / 8)) * 8;
-      const int key = kt0 + row;
-      const bf16 *src = key < a.P8
-                            ? a.kb_cache + ((long)h * a.cap_cache + key) * D
-                            : a.kb_stage + ((long)h * a.cap_stage + (key - a.P8)) * D;
-      *reinterpret_cast<uint4 *>(&Ks[row * KS + col]) = *reinterpret_cast<const uint4 *>(src + col);
+    if (t >= t_begin) {
+      __syncthreads();  // every wave is done with the previous tile
+#pragma unroll
+      for (int u = 0; u < KCH; ++u) *reinterpret_cast<u32x4 *>(&Ks[k_lds[u]]) = kreg[u];
+#pragma unroll
+      for (int u = 0; u < VCH; ++u) {
+        *reinterpret_cast<u32x2 *>(&Vs[v_lds[u]]) = kreg_lo(vreg[u]);
+        *reinterpret_cast<u32x2 *>(&Vs[v_lds[u] + 4]) = kreg_hi(vreg[u]);
+      }
+      __syncthreads();
     }
-    for (int cc = threadIdx.x; cc < D * (BN / 8); cc += NT) {
-      const int dim = cc / (BN / 8), kc = (cc % (BN / 8)) * 8;
-      const int key = kt0 + kc;
-      const bf16 *src = key < a.P8
-                            ? a.vt_cache + ((long)h * D + dim) * a.cap_cache + key
-                            : a.vt_stage + ((long)h * D + dim) * a.cap_stage + (key - a.P8);
-      const uint4 v = *reinterpret_cast<const uint4 *>(src);
-      *reinterpret_cast<uint2 *>(&Vs[dim * VS + kc]) = make_uint2(v.x, v.y);
-      *reinterpret_cast<uint2 *>(&Vs[dim * VS + kc + 4]) = make_uint2(v.z, v.w);
+    if (t + 1 < t_end) {
+      const int nk = kt0 + BN;
+      const bool from_cache = nk < a.P8;
+      const bf16 *kt = from_cache ? kb_c + (long)nk * D : kb_s + (long)(nk - a.P8) * D;
+      const bf16 *vt = from_cache ? vt_c + nk : vt_s + (nk - a.P8);
+      const long vstride = from_cache ? a.cap_cache : a.cap_stage;
+#pragma unroll
+      for (int u = 0; u < KCH; ++u) kreg[u] = *reinterpret_cast<const u32x4 *>(kt + k_row[u]);
+#pragma unroll
+      for (int u = 0; u < VCH; ++u)
+        vreg[u] = *reinterpret_cast<const u32x4 *>(vt + (long)v_dim[u] * vstride + v_kc[u]);
     }
-    __syncthreads();
+    if (t < t_begin) continue;
 
     const bool active = wave_live && !(a.causal && kt0 > wave_max_q) &&
                         !(a.window > 0 && kt0 + BN - 1 + a.window <= wave_min_q);
@@ -160,25 +202,22 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
     const bool need_mask = (a.causal && kt0 + BN - 1 > wave_min_q) ||
                            (a.window > 0 && kt0 + a.window <= wave_max_q) ||
                            (kt0 + BN > key_total);
-    // The masked scores go to a copy: writing -inf in place into the MFMA
+    // Masked scores go to a copy: writing -inf in place into the MFMA
     // accumulator registers gave wrong results on masked tiles.
     float sc[KB][16];
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) sc[kb][i] = sacc[kb][i];
-    if (need_mask) {
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
+      for (int i = 0; i < 16; ++i) {
+        float v = sacc[kb][i];
+        if (need_mask) {
           const int key = kt0 + kb * 32 + 8 * (i >> 2) + 4 * hl + (i & 3);
           const bool masked = (a.causal && key > q_abs) ||
                               (a.window > 0 && key + a.window <= q_abs) || key >= key_total;
-          if (masked) sc[kb][i] = NEG_INF;
+          if (masked) v = NEG_INF;
         }
+        sc[kb][i] = v;
       }
-    }
     float tmax = NEG_INF;
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb)
