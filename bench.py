@@ -45,6 +45,20 @@ def prefill_flops(s: int, hq=HQ, d=D) -> float:
     return 4.0 * d * hq * s * (s + 1) / 2
 
 
+TRAFFIC_PROFILE = ROOT / "profiles" / "decode_b1_hbm_traffic.md"
+
+
+def measured_traffic():
+    """HBM bytes per decode launch from the committed calibrated counter summary."""
+    try:
+        for line in TRAFFIC_PROFILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -340,7 +354,9 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(d1["attn_kernel_GBps"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
+            "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, calibrated on a 256 MiB copy "
+                              "(profiles/decode_b1_hbm_traffic.md)",
             "kernel": "one decode attention launch = decode_split_kernel<128,3,3> + decode_combine_kernel<128,3>; "
                       "event-timed average over 28 back-to-back launches per graph replay",
         },
