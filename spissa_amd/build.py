@@ -38,9 +38,16 @@ COMMON = [
 ]
 
 
+# Per-source additions. prefill_wide.hip keeps MFMA results in VGPRs: its
+# score accumulators feed VALU code, and the AGPR form round-trips them.
+EXTRA = {
+    "prefill_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: Path, verbose: bool) -> Path:
     obj = OBJ / (src.stem + ".o")
-    cmd = [HIPCC, *COMMON, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *COMMON, *EXTRA.get(src.name, []), "-c", str(src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -427,7 +427,7 @@ __global__ __launch_bounds__(1024) void decode_combine_kernel(const DecodeArgs a
     if (a.app_kb[b]) {
       const long cap = a.app_cap[b];
       a.app_kb[b][((long)h * cap + P) * D + tid] = (bf16)kd;
-      a.app_vt[b][((long)h * D + tid) * cap + P] = (bf16)vd;
+      a.app_vt[b][((long)h * D + tid) * cap + vt_key_slot(P)] = (bf16)vd;
     }
   }
 }

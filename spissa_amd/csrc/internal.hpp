@@ -24,6 +24,15 @@ constexpr int kMaxDecodeSplits = 512;
 // multiple of it.
 constexpr int kPrefillTileAlign = 64;
 
+// Key order of the transposed bf16 V operand (the cache shadow's vt and the
+// prefill staging buffer): inside every group of 16 keys, keys 4-7 and 8-11
+// trade places, so that the 8 keys one MFMA lane contributes to a 16-key step
+// of O^T += V^T P^T (keys 0-3 and 8-11, or 4-7 and 12-15, as the score
+// accumulator holds them) are 16 contiguous bytes. The map is its own inverse.
+__host__ __device__ constexpr long vt_key_slot(long key) {
+  return (key & ~12L) | ((key & 4) << 1) | ((key & 8) >> 1);
+}
+
 struct SeqDesc {
   const float *k;  // cache keys   [max_seq, Hkv, D] (may be null when past == 0)
   const float *v;  // cache values [max_seq, Hkv, D]
@@ -32,8 +41,8 @@ struct SeqDesc {
 };
 
 struct DecodeArgs {
-  float *q;            // [B, Hq, D]; rotated in place when rope_cos is set
-  float *cur_k;        // [B, Hkv, D]: the new token's key; rotated in place with q
+  float *q;            // [B, Hq, D]; read only (rotated in registers when rope_cos is set)
+  float *cur_k;        // [B, Hkv, D]: the new token's key; read only
   const float *cur_v;  // [B, Hkv, D]
   float *out;          // [B, Hq, D]
   float *partial;      // [B, Hkv, HB, max_splits] entries of RB*(D+2) floats
@@ -66,15 +75,15 @@ struct PrefillArgs {
   // the staging buffer; P8 is a multiple of kPrefillTileAlign, so no key tile
   // straddles the two.
   const bf16 *kb_cache;  // [Hkv, cap_cache, D]
-  const bf16 *vt_cache;  // [Hkv, D, cap_cache]
+  const bf16 *vt_cache;  // [Hkv, D, cap_cache], keys in vt_key_slot order
   const bf16 *kb_stage;  // [Hkv, cap_stage, D], key 0 of the buffer is absolute key P8
-  const bf16 *vt_stage;  // [Hkv, D, cap_stage]
+  const bf16 *vt_stage;  // [Hkv, D, cap_stage], keys in vt_key_slot order
   long cap_cache, cap_stage;
   int P, P8, S, Hq, Hkv, R;
   int causal, window;
   int *err;
   float qk_scale_log2;  // softmax scale * log2(e), applied to the f32 scores
-  int n_qblocks;        // query blocks of 32 positions
+  int n_qblocks;        // query blocks of one workgroup (set by the launcher)
 };
 
 struct GenericArgs {
@@ -103,6 +112,8 @@ hipError_t launch_stage_bf16(hipStream_t st, const float *k_rows, const float *v
                              size_t dst_first, size_t dst_cap);
 hipError_t launch_decode(hipStream_t st, const DecodeArgs &a, int D, int RB);
 hipError_t launch_prefill(hipStream_t st, const PrefillArgs &a, int D);
+// head_dim 64 and 128 (prefill_wide.hip); launch_prefill dispatches to it.
+hipError_t launch_prefill_wide(hipStream_t st, const PrefillArgs &a, int D);
 hipError_t launch_generic(hipStream_t st, const GenericArgs &a);
 
 // Keys per split of a decode launch: total_rows = key rows summed over all

@@ -1,6 +1,7 @@
-// prefill.hip -- causal GQA prefill (rotary.rs:335-415 with query_len > 1,
-// including chunked prefill against a cache and the sliding-window extension)
-// as a bf16-MFMA flash-attention kernel for gfx950. Inputs and outputs are
+// prefill.hip -- causal GQA prefill for head_dim 256 (rotary.rs:335-415 with
+// query_len > 1, including chunked prefill against a cache and the
+// sliding-window extension) as a bf16-MFMA flash-attention kernel for gfx950,
+// and the prefill launcher (head_dim 64 and 128 run prefill_wide.hip). Inputs and outputs are
 // f32; Q is rounded to bf16 in registers, K and V are read from bf16 copies
 // (the cache's bf16 shadow for keys already cached, a staging buffer for the
 // rest); scores, softmax state and the output accumulate in f32.
@@ -73,7 +74,9 @@ __global__ __launch_bounds__(RB *NPB * 64, D >= 256 ? 1 : 2) void prefill_kernel
   bid /= (a.Hkv * HB);
   const int qt = a.n_qblocks - 1 - bid;  // longest rows first
   const int h = hh / HB, hb = hh % HB;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // The wave index is uniform: readfirstlane keeps it (and all that derives
+  // from it) in scalar registers and wave-level branches uniform.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int r = wave % RB, pb = wave / RB;
   const int head = h * a.R + hb * RB + r;
   const int p0 = qt * WGQ;
@@ -254,12 +257,14 @@ __global__ __launch_bounds__(RB *NPB * 64, D >= 256 ? 1 : 2) void prefill_kernel
       l += ls;
 #pragma unroll
       for (int d = 0; d < DB; ++d) {
-        const bf16 *vrow = &Vs[(d * 32 + lq) * VS + kb * 32 + 4 * hl];
+        // V^T rows hold keys in vt_key_slot order: this lane's 8 keys of each
+        // 16-key step are contiguous.
+        const bf16 *vrow = &Vs[(d * 32 + lq) * VS + kb * 32 + 8 * hl];
         const bf16x8 va = cat(*reinterpret_cast<const bf16x4 *>(vrow),
-                              *reinterpret_cast<const bf16x4 *>(vrow + 8));
+                              *reinterpret_cast<const bf16x4 *>(vrow + 4));
         oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pa, oacc[d], 0, 0, 0);
         const bf16x8 vb = cat(*reinterpret_cast<const bf16x4 *>(vrow + 16),
-                              *reinterpret_cast<const bf16x4 *>(vrow + 24));
+                              *reinterpret_cast<const bf16x4 *>(vrow + 20));
         oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vb, pb, oacc[d], 0, 0, 0);
       }
     }
@@ -312,8 +317,8 @@ bool prefill_supported(int D) { return D == 64 || D == 128 || D == 256; }
 
 hipError_t launch_prefill(hipStream_t st, const PrefillArgs &a, int D) {
   switch (D) {
-    case 64: return launch_d<64>(st, a);
-    case 128: return launch_d<128>(st, a);
+    case 64:
+    case 128: return launch_prefill_wide(st, a, D);
     case 256: return launch_d<256>(st, a);
     default: return hipErrorInvalidValue;
   }

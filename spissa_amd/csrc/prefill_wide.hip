@@ -1,0 +1,449 @@
+// prefill_wide.hip -- causal GQA prefill for head_dim 64 and 128
+// (rotary.rs:335-415 with query_len > 1, including chunked prefill against a
+// cache and the sliding-window extension) as a bf16-MFMA flash-attention
+// kernel for gfx950. Inputs and outputs are f32; Q is rounded to bf16 in
+// registers, K and V are read from bf16 copies (the cache's bf16 shadow for
+// tiles below P8, the staging buffer for the rest); scores, softmax state and
+// the output accumulate in f32.
+//
+// Work split. Each wave owns QB 32-query blocks of one query head (QB = 1 in
+// the launched configurations), and the four waves of a workgroup share one KV
+// head: four heads of a group, two heads with two blocks each, or one head
+// with four blocks. Two waves run per SIMD (at most 256 VGPRs each).
+//
+// Per key tile of BN keys and per query block a wave computes
+//   S^T = K Q^T   v_mfma_f32_32x32x16_bf16, A = K rows from LDS, B = Q^T in
+//                 registers; the accumulator puts one query per lane (lane &
+//                 31) and 16 of its keys per lane, so row max and sum are
+//                 lane-local plus one v_permlane32_swap;
+//   O^T += V^T P^T  A = V^T from LDS, B = P^T straight from the score
+//                 registers (keys of the V^T operand are stored in
+//                 vt_key_slot order, so each lane's 8 keys are 16 contiguous
+//                 bytes).
+// Copies. K and V^T tiles go global -> LDS with global_load_lds_dwordx4 (no
+// staging registers) into two alternating buffers each. The loop is
+// software-pipelined one tile deep: in step t the copies of K(t+2) and V(t+1)
+// are in flight while the exponentials of tile t run on the VALU interleaved
+// (sched_group_barrier) with the MFMAs of S(t+1) = K(t+1) Q^T, then
+// O^T += V(t)^T P(t)^T; one barrier per step.
+// Tiles are unpadded; the 16-byte chunks of each row are XOR-swizzled within
+// the row by swz(row), chosen so that the 8 consecutive rows one LDS read
+// serves together (same chunk index) hit 8 distinct 16-byte bank groups:
+//   K tile   [BN keys][D]: chunk c of key row r at byte r*2D  + 16*(c ^ swz(r))
+//   V^T tile [D][BN keys]: chunk c of dim row d at byte d*2BN + 16*(c ^ swz(d))
+// Softmax. The exponent reference m of a row is raised only when the row
+// maximum exceeds it by more than 2^8 (in the log2 domain), so exponentials
+// stay below 256 and the O accumulators are rescaled a handful of times per
+// row instead of on most tiles; O and the sum share m, so O / sum is exact
+// softmax arithmetic.
+// This file is compiled with MFMA results in VGPRs (-amdgpu-mfma-vgpr-form):
+// the score accumulators feed VALU code directly instead of round-tripping
+// through AGPRs.
+#include <type_traits>
+
+#include "internal.hpp"
+
+namespace spissa {
+
+namespace {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr float NEG_INF = -__builtin_inff();
+// Largest growth of a row maximum (log2 domain) absorbed without rescaling.
+constexpr float kRescaleSlack = 8.0f;
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// NaN-propagating maximum (v_maximum_f32): no input canonicalisation, and a
+// NaN score reaches the denominator check.
+__device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
+__device__ __forceinline__ float xor32_max(float v) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Copies 16 bytes per lane from src into LDS at lds_base + 16 * lane.
+__device__ __forceinline__ void dma16(const char *src, char *lds_base) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void *)lds_base, 16, 0, 0);
+}
+
+// Waits for this wave's outstanding global -> LDS copies.
+__device__ __forceinline__ void wait_copies() {
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt and lgkmcnt unconstrained
+}
+
+// XOR swizzle of a row of NC 16-byte chunks (NC = 4, 8 or 16), staying below
+// NC. For a fixed chunk index, any 8 aligned consecutive rows land in 8
+// distinct 16-byte groups modulo 128 bytes and any 16 aligned consecutive rows
+// in 16 distinct groups modulo 256 bytes, so an LDS read is conflict-free
+// whether the hardware serves 8 lanes per 128 bytes or 16 lanes per 256. The
+// swizzle of row 32 b + l does not depend on b.
+template <int NC>
+__device__ __forceinline__ constexpr int swz(int row) {
+  static_assert(NC == 4 || NC == 8 || NC == 16, "row width");
+  return NC == 16 ? (row & 15) : NC == 8 ? ((row ^ ((row >> 3) & 1)) & 7) : (((row >> 1) ^ (row >> 2)) & 3);
+}
+
+template <int D, int BN, int NW>
+struct Geom {
+  static constexpr int KBYTES = BN * D * 2;
+  static constexpr int VBYTES = D * BN * 2;
+  static constexpr int KDMA = KBYTES / 1024 / NW;  // K copies per wave per tile
+  static constexpr int VDMA = VBYTES / 1024 / NW;  // V^T copies per wave per tile
+  static constexpr int DT = D / 16;                // 16-dim steps of S^T = K Q^T
+  static constexpr int KB = BN / 32;               // 32-key score blocks
+  static constexpr int KS = BN / 16;               // 16-key steps of O^T += V^T P^T
+  static constexpr int DB = D / 32;                // 32-dim output blocks
+  static constexpr int KNC = D / 8;                // 16-byte chunks per K row
+  static constexpr int VNC = BN / 8;               // 16-byte chunks per V^T row
+  static_assert(KDMA * NW * 1024 == KBYTES && VDMA * NW * 1024 == VBYTES, "tile/wave split");
+};
+
+// S^T of one key tile for the wave's QB query blocks; kbuf is the K tile in LDS.
+template <int D, int BN, int QB>
+__device__ __forceinline__ void score_tile(f32x16 (&s)[QB][BN / 32], const char *kbuf,
+                                           const unsigned (&k_rd)[D / 16],
+                                           const bf16x8 (&qf)[QB][D / 16]) {
+  constexpr int DT = D / 16, KB = BN / 32;
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[qb][kb][i] = 0.0f;
+#pragma unroll
+  for (int tt = 0; tt < DT; ++tt)
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      const bf16x8 kf = *reinterpret_cast<const bf16x8 *>(kbuf + kb * 64 * D + k_rd[tt]);
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb)
+        s[qb][kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[qb][tt], s[qb][kb], 0, 0, 0);
+    }
+}
+
+}  // namespace
+
+// QB query blocks of 32 per wave (1 or 2); two waves per SIMD unless the
+// accumulators of two 128-wide blocks need the whole register file.
+template <int D, int RB, int NPB, int BN, int QB>
+__global__ __launch_bounds__(RB *NPB * 64, (QB == 1 || D <= 64) ? 2 : 1) void prefill_wide_kernel(const PrefillArgs a) {
+  constexpr int NW = RB * NPB;
+  constexpr int WQ = QB * 32;  // queries per wave
+  constexpr int WGQ = NPB * WQ;
+  using G = Geom<D, BN, NW>;
+  constexpr int DT = G::DT, KB = G::KB, KS = G::KS, DB = G::DB;
+
+  // Four separate LDS objects (not one array): the compiler then knows that
+  // copies into one buffer do not alias reads of another and does not wait
+  // for the copies before every LDS read.
+  __shared__ __attribute__((aligned(1024))) char k_lds0[G::KBYTES];
+  __shared__ __attribute__((aligned(1024))) char k_lds1[G::KBYTES];
+  __shared__ __attribute__((aligned(1024))) char v_lds0[G::VBYTES];
+  __shared__ __attribute__((aligned(1024))) char v_lds1[G::VBYTES];
+
+  const int HB = a.R / RB;
+  int bid = blockIdx.x;
+  const int hh = bid % (a.Hkv * HB);
+  bid /= (a.Hkv * HB);
+  const int qt = a.n_qblocks - 1 - bid;  // longest rows first
+  const int h = hh / HB, hb = hh % HB;
+  // The wave index is uniform: readfirstlane keeps it (and all that derives
+  // from it) in scalar registers and wave-level branches uniform.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int r = wave % RB, pb = wave / RB;
+  const int head = h * a.R + hb * RB + r;
+  const int p0 = qt * WGQ;
+  const int wp0 = p0 + pb * WQ;
+  const int lq = lane & 31, hl = lane >> 5;
+  const int key_total = a.P + a.S;
+
+  int key_end = key_total;
+  if (a.causal) key_end = min(key_total, a.P + min(a.S, p0 + WGQ));
+  int key_begin = 0;
+  if (a.window > 0) key_begin = max(0, a.P + p0 - a.window + 1);
+  const int t_begin = key_begin / BN;
+  const int t_end = (key_end + BN - 1) / BN;
+
+  // Q^T (B operand): lane holds query lq of block qb, dims 16t + 8hl + [0,8).
+  bf16x8 qf[QB][DT];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const int pos = min(wp0 + 32 * qb + lq, a.S - 1);
+    const float *qp = a.q + ((long)pos * a.Hq + head) * D + 8 * hl;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      const float4 x0 = *reinterpret_cast<const float4 *>(qp + 16 * t);
+      const float4 x1 = *reinterpret_cast<const float4 *>(qp + 16 * t + 4);
+      bf16x8 v;
+      v[0] = (bf16)x0.x; v[1] = (bf16)x0.y; v[2] = (bf16)x0.z; v[3] = (bf16)x0.w;
+      v[4] = (bf16)x1.x; v[5] = (bf16)x1.y; v[6] = (bf16)x1.z; v[7] = (bf16)x1.w;
+      qf[qb][t] = v;
+    }
+  }
+  f32x16 oacc[QB][DB];
+  float m[QB], l[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+#pragma unroll
+    for (int d = 0; d < DB; ++d)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) oacc[qb][d][i] = 0.0f;
+    m[qb] = NEG_INF;
+    l[qb] = 0.0f;
+  }
+
+  // LDS byte offsets of this lane's fragments (key block 0 / dim block 0).
+  // (Rows of a fragment are 32 * block + lq, and 32 * block leaves swz unchanged.)
+  unsigned k_rd[DT], v_rd[KS];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) k_rd[t] = lq * 2 * D + 16 * ((2 * t + hl) ^ swz<G::KNC>(lq));
+#pragma unroll
+  for (int t = 0; t < KS; ++t) v_rd[t] = lq * 2 * BN + 16 * ((2 * t + hl) ^ swz<G::VNC>(lq));
+
+  // Source of this lane's copies: copy j of the wave fills LDS bytes
+  // [(wave + j*NW) * 1024, +1024) of a tile; lane l writes its 16 bytes at
+  // +16 l, i.e. position p of K row `row` (V^T: dim row d), which holds chunk
+  // p ^ swz(row) of that row. Every source chunk lies inside the tile's row.
+  unsigned k_src[G::KDMA], v_row[G::VDMA], v_col[G::VDMA];
+#pragma unroll
+  for (int j = 0; j < G::KDMA; ++j) {
+    const int byte = (wave + j * NW) * 1024 + lane * 16;
+    const int row = byte / (2 * D), p = (byte % (2 * D)) / 16;
+    k_src[j] = (unsigned)(row * D + 8 * (p ^ swz<G::KNC>(row))) * 2u;
+  }
+#pragma unroll
+  for (int j = 0; j < G::VDMA; ++j) {
+    const int byte = (wave + j * NW) * 1024 + lane * 16;
+    const int d = byte / (2 * BN), p = (byte % (2 * BN)) / 16;
+    v_row[j] = d;
+    v_col[j] = 8 * (p ^ swz<G::VNC>(d));
+  }
+  const char *kb_c = reinterpret_cast<const char *>(a.kb_cache + (long)h * a.cap_cache * D);
+  const char *kb_s = reinterpret_cast<const char *>(a.kb_stage + (long)h * a.cap_stage * D);
+  const char *vt_c = reinterpret_cast<const char *>(a.vt_cache + (long)h * D * a.cap_cache);
+  const char *vt_s = reinterpret_cast<const char *>(a.vt_stage + (long)h * D * a.cap_stage);
+
+  // Tiles below P8 come from the cache shadow, the others from staging (P8 is
+  // a multiple of the tile width, so the choice is uniform per tile).
+  auto copy_k = [&](int t, char *dst) {
+    const int nk = t * BN;
+    const char *src = nk < a.P8 ? kb_c + (long)nk * D * 2 : kb_s + (long)(nk - a.P8) * D * 2;
+#pragma unroll
+    for (int j = 0; j < G::KDMA; ++j) dma16(src + k_src[j], dst + (wave + j * NW) * 1024);
+  };
+  auto copy_v = [&](int t, char *dst) {
+    const int nk = t * BN;
+    const bool cached = nk < a.P8;
+    const char *src = cached ? vt_c + (long)nk * 2 : vt_s + (long)(nk - a.P8) * 2;
+    const unsigned stride = (unsigned)(cached ? a.cap_cache : a.cap_stage);
+#pragma unroll
+    for (int j = 0; j < G::VDMA; ++j) dma16(src + (v_row[j] * stride + v_col[j]) * 2u, dst + (wave + j * NW) * 1024);
+  };
+
+  // Visible keys [vis_lo, vis_hi] of this lane's two queries.
+  int vis_lo[QB], vis_hi[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const int q_abs = a.P + wp0 + 32 * qb + lq;
+    vis_hi[qb] = a.causal ? min(q_abs, key_total - 1) : key_total - 1;
+    vis_lo[qb] = a.window > 0 ? q_abs - a.window + 1 : 0;
+  }
+  const int wave_min_q = a.P + wp0;
+  const int wave_max_q = a.P + min(wp0 + WQ - 1, a.S - 1);
+  const float c = a.qk_scale_log2;
+
+  // One pipelined step on tile t with scores in `cur`: copies of K(t+2) and
+  // V(t+1); mask and softmax of tile t; S(t+1) into `nxt` (also on the last
+  // tile, where it reads a stale buffer and is never used: keeping it
+  // unconditional lets its MFMAs interleave with the softmax VALU work);
+  // O^T += V(t)^T P(t)^T. O selects the buffers.
+  auto step = [&](auto O_, int t, f32x16 (&cur)[QB][KB], f32x16 (&nxt)[QB][KB]) {
+    constexpr int O = decltype(O_)::value;
+    char *const k_this = O ? k_lds1 : k_lds0;  // receives K(t+2)
+    char *const k_next = O ? k_lds0 : k_lds1;  // holds K(t+1)
+    char *const v_this = O ? v_lds1 : v_lds0;  // holds V(t)
+    char *const v_next = O ? v_lds0 : v_lds1;  // receives V(t+1)
+    if (t + 2 < t_end) copy_k(t + 2, k_this);
+    if (t + 1 < t_end) copy_v(t + 1, v_next);
+    const int kt0 = t * BN;
+
+    // Masked keys become -inf in a copy of the scores.
+    float sc[QB][KB][16];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sc[qb][kb][i] = cur[qb][kb][i];
+    const bool need_mask = (a.causal && kt0 + BN - 1 > wave_min_q) ||
+                           (a.window > 0 && kt0 + a.window <= wave_max_q) || (kt0 + BN > key_total);
+    if (need_mask) {
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        const int lo = vis_lo[qb] - kt0 - 4 * hl, hi = vis_hi[qb] - kt0 - 4 * hl;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int kk = kb * 32 + 8 * (i >> 2) + (i & 3);
+            sc[qb][kb][i] = (kk < lo || kk > hi) ? NEG_INF : sc[qb][kb][i];
+          }
+      }
+    }
+
+    // Softmax of tile t, part 1: row maxima, exponent references, and the
+    // (rare) rescale of O.
+    float alpha[QB], ms[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      float mx = sc[qb][0][0];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = vmax(mx, sc[qb][kb][i]);
+      mx = xor32_max(mx) * c;
+      const bool raise = mx > m[qb] + kRescaleSlack;
+      const float mnew = raise ? mx : m[qb];
+      ms[qb] = mnew == NEG_INF ? 0.0f : mnew;
+      alpha[qb] = fast_exp2(m[qb] - ms[qb]);
+      m[qb] = mnew;
+      if (__ballot(raise)) {
+#pragma unroll
+        for (int d = 0; d < DB; ++d)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) oacc[qb][d][i] *= alpha[qb];
+      }
+    }
+
+    // Part 2: probabilities (bf16 B operand of PV) on the VALU, interleaved
+    // with the MFMAs of S(t+1), whose two accumulation chains would otherwise
+    // wait on each other.
+    float psum[QB];
+    bf16x8 pf[QB][KS];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      psum[qb] = 0.0f;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        bf16x8 p;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float pv = fast_exp2(fmaf(sc[qb][ks >> 1][8 * (ks & 1) + j], c, -ms[qb]));
+          psum[qb] += pv;
+          p[j] = (bf16)pv;
+        }
+        pf[qb][ks] = p;
+      }
+    }
+    score_tile<D, BN, QB>(nxt, k_next, k_rd, qf);
+    {
+      constexpr int NMFMA = QB * KB * DT;       // MFMAs of S(t+1)
+      constexpr int NREAD = KB * DT;            // K fragment reads
+      constexpr int NVALU = QB * BN * 7 / 2;    // about 3.5 VALU per score (fma, exp, add, cvt)
+      constexpr int PER = (NVALU + NMFMA - 1) / NMFMA;
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // two fragment reads ahead
+#pragma unroll
+      for (int i = 0; i < NMFMA; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        if (i + 2 < NREAD * QB && (i % QB) == QB - 1) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, PER, 0);  // softmax VALU work
+      }
+    }
+
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) l[qb] = l[qb] * alpha[qb] + psum[qb];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int d = 0; d < DB; ++d) {
+        const bf16x8 vf = *reinterpret_cast<const bf16x8 *>(v_this + d * 64 * BN + v_rd[ks]);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb)
+          oacc[qb][d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[qb][ks], oacc[qb][d], 0, 0, 0);
+      }
+    wait_copies();
+    __syncthreads();
+  };
+
+  // Prologue: K(t0), V(t0), K(t0+1) copied; S(t0) computed.
+  f32x16 sa[QB][KB], sb[QB][KB];
+  copy_k(t_begin, k_lds0);
+  copy_v(t_begin, v_lds0);
+  if (t_begin + 1 < t_end) copy_k(t_begin + 1, k_lds1);
+  wait_copies();
+  __syncthreads();
+  score_tile<D, BN, QB>(sa, k_lds0, k_rd, qf);
+  __syncthreads();  // every wave is done with K(t0) before K(t0+2) lands in its buffer
+
+  for (int t = t_begin; t < t_end; t += 2) {
+    step(std::integral_constant<int, 0>(), t, sa, sb);
+    if (t + 1 < t_end) step(std::integral_constant<int, 1>(), t + 1, sb, sa);
+  }
+
+  // ---- epilogue: O = O^T / l ----
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const int pos = wp0 + 32 * qb + lq;
+    const float lt = xor32_sum(l[qb]);
+    if (pos < a.S) {
+      // positive, finite and non-zero, tested on the bits (NaN fails it)
+      if (hl == 0 && !(__float_as_uint(lt) - 1u < 0x7f7fffffu)) atomicOr(a.err, kDevErrSoftmaxDenominator);
+      const float inv = 1.0f / lt;
+      float *op = a.out + ((long)pos * a.Hq + head) * D + 4 * hl;
+#pragma unroll
+      for (int d = 0; d < DB; ++d)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float4 v = make_float4(oacc[qb][d][4 * g] * inv, oacc[qb][d][4 * g + 1] * inv,
+                                 oacc[qb][d][4 * g + 2] * inv, oacc[qb][d][4 * g + 3] * inv);
+          *reinterpret_cast<float4 *>(op + d * 32 + 8 * g) = v;
+        }
+    }
+  }
+}
+
+namespace {
+
+template <int D, int RB, int NPB, int BN, int QB>
+hipError_t launch_shape(hipStream_t st, PrefillArgs a) {
+  constexpr int WGQ = NPB * QB * 32;
+  a.n_qblocks = (a.S + WGQ - 1) / WGQ;
+  const long blocks = (long)a.n_qblocks * a.Hkv * (a.R / RB);
+  hipLaunchKernelGGL((prefill_wide_kernel<D, RB, NPB, BN, QB>), dim3((unsigned)blocks), dim3(RB * NPB * 64), 0, st,
+                     a);
+  return hipGetLastError();
+}
+
+// Four-wave workgroups, 32 queries per wave, 64-key tiles, two waves per
+// SIMD: four heads of the KV group, two heads with two blocks, or one head
+// with four blocks. (64 queries per wave halves the LDS fragment reads per
+// MFMA but, at head_dim 128, needs more than 256 VGPRs and measured slower;
+// at head_dim 64 it halves the workgroup count, which a 2048-token prefill
+// cannot afford.)
+template <int D>
+hipError_t launch_d(hipStream_t st, const PrefillArgs &a) {
+  if (a.R % 4 == 0) return launch_shape<D, 4, 1, 64, 1>(st, a);
+  if (a.R % 2 == 0) return launch_shape<D, 2, 2, 64, 1>(st, a);
+  return launch_shape<D, 1, 4, 64, 1>(st, a);
+}
+
+}  // namespace
+
+hipError_t launch_prefill_wide(hipStream_t st, const PrefillArgs &a, int D) {
+  switch (D) {
+    case 64: return launch_d<64>(st, a);
+    case 128: return launch_d<128>(st, a);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace spissa

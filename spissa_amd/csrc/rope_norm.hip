@@ -90,9 +90,10 @@ __global__ void gemma_prologue_kernel(const float *__restrict__ cos_tab,
 }
 
 // Converts n rows of K and V ([n, H, D] f32) to the prefill operand layouts:
-// kb [H, cap, D] bf16 (head-major K) and vt [H, D, cap] bf16 (transposed V),
-// at buffer positions dst_first + i. Rows with i >= n (up to the tile's end)
-// are written as zeros so padded key tiles read finite data.
+// kb [H, cap, D] bf16 (head-major K) and vt [H, D, cap] bf16 (transposed V,
+// key p stored at slot vt_key_slot(p)), at buffer positions dst_first + i.
+// Rows with i >= n (up to the tile's end) are written as zeros so padded key
+// tiles read finite data.
 // Grid: (ceil(n_pad/64), H, ceil(D/64)), 256 threads.
 __global__ void stage_bf16_kernel(const float *__restrict__ k_rows,
                                   const float *__restrict__ v_rows, long n, long n_pad, int H,
@@ -120,7 +121,7 @@ __global__ void stage_bf16_kernel(const float *__restrict__ k_rows,
   for (int dd = ty; dd < 64; dd += 4) {
     int d = d0 + dd;
     long i = i0 + tx;
-    if (d < D && i < n_pad) vt[((long)h * D + d) * cap + dst_first + i] = (bf16)tile[tx][dd];
+    if (d < D && i < n_pad) vt[((long)h * D + d) * cap + vt_key_slot(dst_first + i)] = (bf16)tile[tx][dd];
   }
 }
 
