@@ -304,7 +304,7 @@ template <int D, int RB>
 __global__ __launch_bounds__(1024) void decode_combine_kernel(const DecodeArgs a) {
   constexpr int HALF = D / 2;
   constexpr int ENTRY = RB * (D + 2);
-  constexpr int OUTS = 64, SL = 16, UNROLL = 4;
+  constexpr int OUTS = 64, SL = 16, UNROLL = 8;  // one load round up to 128 splits
   __shared__ float s_m[SL][OUTS], s_l[SL][OUTS], s_o[SL][OUTS];
   __shared__ float s_dot[RB * D / 64];
   __shared__ float s_new[RB];

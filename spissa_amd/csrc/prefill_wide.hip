@@ -23,9 +23,9 @@
 // Copies. K and V^T tiles go global -> LDS with global_load_lds_dwordx4 (no
 // staging registers) into two alternating buffers each. The loop is
 // software-pipelined one tile deep: in step t the copies of K(t+2) and V(t+1)
-// are in flight while the exponentials of tile t run on the VALU interleaved
-// (sched_group_barrier) with the MFMAs of S(t+1) = K(t+1) Q^T, then
-// O^T += V(t)^T P(t)^T; one barrier per step.
+// are in flight while the exponentials of tile t run on the VALU next to the
+// MFMAs of S(t+1) = K(t+1) Q^T, then O^T += V(t)^T P(t)^T; one barrier per
+// step.
 // Tiles are unpadded; the 16-byte chunks of each row are XOR-swizzled within
 // the row by swz(row), chosen so that the 8 consecutive rows one LDS read
 // serves together (same chunk index) hit 8 distinct 16-byte bank groups:
@@ -324,9 +324,8 @@ __global__ __launch_bounds__(RB *NPB * 64, (QB == 1 || D <= 64) ? 2 : 1) void pr
       }
     }
 
-    // Part 2: probabilities (bf16 B operand of PV) on the VALU, interleaved
-    // with the MFMAs of S(t+1), whose two accumulation chains would otherwise
-    // wait on each other.
+    // Part 2: probabilities (bf16 B operand of PV) on the VALU; the MFMAs of
+    // S(t+1) that follow are independent of them and overlap.
     float psum[QB];
     bf16x8 pf[QB][KS];
 #pragma unroll
@@ -345,19 +344,6 @@ __global__ __launch_bounds__(RB *NPB * 64, (QB == 1 || D <= 64) ? 2 : 1) void pr
       }
     }
     score_tile<D, BN, QB>(nxt, k_next, k_rd, qf);
-    {
-      constexpr int NMFMA = QB * KB * DT;       // MFMAs of S(t+1)
-      constexpr int NREAD = KB * DT;            // K fragment reads
-      constexpr int NVALU = QB * BN * 7 / 2;    // about 3.5 VALU per score (fma, exp, add, cvt)
-      constexpr int PER = (NVALU + NMFMA - 1) / NMFMA;
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // two fragment reads ahead
-#pragma unroll
-      for (int i = 0; i < NMFMA; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-        if (i + 2 < NREAD * QB && (i % QB) == QB - 1) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, PER, 0);  // softmax VALU work
-      }
-    }
 
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) l[qb] = l[qb] * alpha[qb] + psum[qb];
