@@ -76,6 +76,12 @@ struct spissa_session {
   DevBuf partial;   // decode split partials
   DevBuf stage;     // prefill bf16 staging of K / V^T
   DevBuf table;     // drop-in RoPE rows
+  DevBuf ppart;     // prefill key-split partials (O, then (m, l))
+  int cus = 256;    // compute units of the device
+  // Buffers replaced by larger ones. They stay allocated until the session
+  // is destroyed, so a HIP graph captured before a workspace grew still
+  // replays on valid memory.
+  std::vector<void *> retired;
   int prefill_precision = SPISSA_PREFILL_BF16;
 };
 
@@ -102,13 +108,10 @@ static int ensure_buf(spissa_session *s, DevBuf &b, size_t bytes, bool zero) {
   size_t want = std::max(bytes, b.bytes + b.bytes / 2);
   want = (want + 4095) & ~(size_t)4095;
   HIP_TRY(hipSetDevice(s->device));
-  if (b.p) {
-    HIP_TRY(hipStreamSynchronize(s->stream));
-    HIP_TRY(hipFree(b.p));
-    b.p = nullptr;
-    b.bytes = 0;
-  }
-  HIP_TRY(hipMalloc(&b.p, want));
+  void *p = nullptr;
+  HIP_TRY(hipMalloc(&p, want));
+  if (b.p) s->retired.push_back(b.p);
+  b.p = p;
   if (zero) {
     HIP_TRY(hipMemsetAsync(b.p, 0, want, s->stream));
     HIP_TRY(hipStreamSynchronize(s->stream));
@@ -133,6 +136,7 @@ extern "C" int spissa_session_create(int device, void *stream, spissa_session **
   HIP_TRY(hipSetDevice(device));
   std::unique_ptr<spissa_session> s(new spissa_session());
   s->device = device;
+  HIP_TRY(hipDeviceGetAttribute(&s->cus, hipDeviceAttributeMultiprocessorCount, device));
   if (stream) {
     s->stream = (hipStream_t)stream;
   } else {
@@ -155,6 +159,8 @@ extern "C" void spissa_session_destroy(spissa_session *s) {
   free_buf(s->partial);
   free_buf(s->stage);
   free_buf(s->table);
+  free_buf(s->ppart);
+  for (void *p : s->retired) (void)hipFree(p);
   if (s->d_err) (void)hipFree(s->d_err);
   if (s->own_stream) (void)hipStreamDestroy(s->stream);
   delete s;
@@ -986,7 +992,29 @@ static int run_prefill(spissa_session *s, const float *d_q, const float *d_k, co
   a.window = (int)c->window;
   a.err = s->d_err;
   a.qk_scale_log2 = (1.0f / sqrtf((float)D)) * 1.4426950408889634f;
+  a.splits = 1;
+  // Key splits when the unsplit grid cannot fill the GPU (short chunks over
+  // long caches, few heads): enough splits for one round of workgroup slots,
+  // each covering at least four key tiles of its workgroup's range.
+  const long base = prefill_base_workgroups(a, D);
+  const long slots = (long)s->cus * prefill_wgs_per_cu(D);
+  if (base < slots) {
+    const int bn = prefill_tile_keys(D), wgq = prefill_wg_queries(a, D);
+    long keys = (long)P + S;  // widest visible key range of one workgroup
+    if (a.window > 0) keys = std::min(keys, (long)a.window + wgq + bn);
+    const long tiles = (keys + bn - 1) / bn + 1;
+    const long want = std::min((slots + base - 1) / base, tiles / 4);
+    if (want >= 2) {
+      a.tps = (int)((tiles + want - 1) / want);
+      a.splits = (int)((tiles + a.tps - 1) / a.tps);
+      const size_t rows = (size_t)a.splits * S * a.Hq;
+      ST_TRY(ensure_buf(s, s->ppart, rows * (D + 2) * sizeof(float), false));
+      a.part_o = (float *)s->ppart.p;
+      a.part_ml = a.part_o + rows * D;
+    }
+  }
   HIP_TRY(launch_prefill(s->stream, a, D));
+  HIP_TRY(launch_prefill_combine(s->stream, a, D));
   return SPISSA_OK;
 }
 

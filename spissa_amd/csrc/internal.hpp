@@ -84,7 +84,23 @@ struct PrefillArgs {
   int *err;
   float qk_scale_log2;  // softmax scale * log2(e), applied to the f32 scores
   int n_qblocks;        // query blocks of one workgroup (set by the launcher)
+  // Key splits (flash-decoding for short chunks over long caches): with
+  // splits > 1, split j of a workgroup covers key tiles [j*tps, (j+1)*tps) of
+  // the workgroup's visible tile range and writes its unnormalised O and
+  // (m, l) per query row to part_o [splits][S][Hq][D] and part_ml
+  // [splits][S][Hq][2] (m in the scaled log2 domain, -inf when the row saw no
+  // key); launch_prefill_combine merges them. splits == 1 writes `out`.
+  int splits, tps;
+  float *part_o, *part_ml;
 };
+
+// Workgroup slots per CU and key-tile width of the prefill kernels, and the
+// queries per workgroup, for choosing key splits.
+int prefill_wgs_per_cu(int D);
+int prefill_tile_keys(int D);
+int prefill_wg_queries(const PrefillArgs &a, int D);
+// Workgroups one (unsplit) prefill launch would have.
+long prefill_base_workgroups(const PrefillArgs &a, int D);
 
 struct GenericArgs {
   const float *q;  // [S, Hq, D]
@@ -112,6 +128,8 @@ hipError_t launch_stage_bf16(hipStream_t st, const float *k_rows, const float *v
                              size_t dst_first, size_t dst_cap);
 hipError_t launch_decode(hipStream_t st, const DecodeArgs &a, int D, int RB);
 hipError_t launch_prefill(hipStream_t st, const PrefillArgs &a, int D);
+// Merges the key splits of a split prefill into `out` (and the error flag).
+hipError_t launch_prefill_combine(hipStream_t st, const PrefillArgs &a, int D);
 // head_dim 64 and 128 (prefill_wide.hip); launch_prefill dispatches to it.
 hipError_t launch_prefill_wide(hipStream_t st, const PrefillArgs &a, int D);
 hipError_t launch_generic(hipStream_t st, const GenericArgs &a);

@@ -72,6 +72,8 @@ __global__ __launch_bounds__(RB *NPB * 64, D >= 256 ? 1 : 2) void prefill_kernel
   int bid = blockIdx.x;
   const int hh = bid % (a.Hkv * HB);
   bid /= (a.Hkv * HB);
+  const int split = bid % a.splits;
+  bid /= a.splits;
   const int qt = a.n_qblocks - 1 - bid;  // longest rows first
   const int h = hh / HB, hb = hh % HB;
   // The wave index is uniform: readfirstlane keeps it (and all that derives
@@ -91,8 +93,12 @@ __global__ __launch_bounds__(RB *NPB * 64, D >= 256 ? 1 : 2) void prefill_kernel
   if (a.causal) key_end = min(key_total, a.P + min(a.S, p0 + WGQ));
   int key_begin = 0;
   if (a.window > 0) key_begin = max(0, a.P + p0 - a.window + 1);
-  const int t_begin = key_begin / BN;
-  const int t_end = (key_end + BN - 1) / BN;
+  int t_begin = key_begin / BN;
+  int t_end = (key_end + BN - 1) / BN;
+  if (a.splits > 1) {  // this split's share of the tiles (empty: m = -inf, l = 0)
+    t_begin += split * a.tps;
+    t_end = min(t_end, t_begin + a.tps);
+  }
 
   // Q as the B operand of S^T = K Q^T: lane holds query lq, dims 16t + 8hl + [0,8).
   bf16x8 qf[D / 16];
@@ -270,8 +276,26 @@ __global__ __launch_bounds__(RB *NPB * 64, D >= 256 ? 1 : 2) void prefill_kernel
     }
   }
 
-  // ---- epilogue: O = O^T / l ----
   const float lt = xor32_sum(l);
+  if (a.splits > 1) {  // unnormalised O and (m, l) of this key split
+    if (pos_ok) {
+      const long row = ((long)split * a.S + my_pos) * a.Hq + head;
+      float *op = a.part_o + row * D + 4 * hl;
+#pragma unroll
+      for (int d = 0; d < DB; ++d)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<float4 *>(op + d * 32 + 8 * g) =
+              make_float4(oacc[d][4 * g], oacc[d][4 * g + 1], oacc[d][4 * g + 2], oacc[d][4 * g + 3]);
+      if (hl == 0) {
+        a.part_ml[row * 2] = m;
+        a.part_ml[row * 2 + 1] = lt;
+      }
+    }
+    return;
+  }
+
+  // ---- epilogue: O = O^T / l ----
   if (pos_ok) {
     if (hl == 0 && !(lt > 0.0f && lt < __builtin_inff())) atomicOr(a.err, kDevErrSoftmaxDenominator);
     const float inv = 1.0f / lt;
@@ -295,7 +319,7 @@ hipError_t launch_cfg(hipStream_t st, PrefillArgs a) {
   constexpr int BN = D >= 256 ? 32 : 64;
   constexpr int WGQ = NPB * 32;
   a.n_qblocks = (a.S + WGQ - 1) / WGQ;
-  const long blocks = (long)a.n_qblocks * a.Hkv * (a.R / RB);
+  const long blocks = (long)a.n_qblocks * a.splits * a.Hkv * (a.R / RB);
   hipLaunchKernelGGL((prefill_kernel<D, RB, NPB, BN>), dim3((unsigned)blocks), dim3(RB * NPB * 64),
                      0, st, a);
   return hipGetLastError();
@@ -314,6 +338,49 @@ hipError_t launch_d(hipStream_t st, const PrefillArgs &a) {
 }  // namespace
 
 bool prefill_supported(int D) { return D == 64 || D == 128 || D == 256; }
+
+// Both kernels launch four-wave workgroups of 32 queries per wave: four heads
+// x 32 queries, two heads x 64, or one head x 128 (launch_d here and in
+// prefill_wide.hip).
+int prefill_wg_queries(const PrefillArgs &a, int) { return a.R % 4 == 0 ? 32 : a.R % 2 == 0 ? 64 : 128; }
+int prefill_wgs_per_cu(int D) { return D >= 256 ? 1 : 2; }
+int prefill_tile_keys(int D) { return D >= 256 ? 32 : 64; }
+
+long prefill_base_workgroups(const PrefillArgs &a, int D) {
+  const int wgq = prefill_wg_queries(a, D);
+  const int rb = 128 / wgq;
+  return (long)((a.S + wgq - 1) / wgq) * a.Hkv * (a.R / rb);
+}
+
+// Merges key splits: per (query row, head), M = max m_j, then
+// O = sum_j O_j 2^(m_j - M), L = sum_j l_j 2^(m_j - M), out = O / L. Splits
+// that saw no key of the row (m_j = -inf) contribute nothing. One workgroup of
+// D threads per (row, head); the error bit is set for an invalid L, as the
+// unsplit kernels do (rotary.rs:560-564).
+__global__ __launch_bounds__(256) void prefill_combine_kernel(const PrefillArgs a, int D) {
+  const long row = blockIdx.x;  // pos * Hq + head
+  const int d = threadIdx.x;
+  const long stride = (long)a.S * a.Hq;
+  float M = -__builtin_inff();
+  for (int j = 0; j < a.splits; ++j) M = fmaxf(M, a.part_ml[(j * stride + row) * 2]);
+  const float Ms = M == -__builtin_inff() ? 0.0f : M;
+  float L = 0.0f, O = 0.0f;
+  for (int j = 0; j < a.splits; ++j) {
+    const float mj = a.part_ml[(j * stride + row) * 2];
+    if (mj == -__builtin_inff()) continue;
+    const float g = __builtin_amdgcn_exp2f(mj - Ms);
+    L = fmaf(a.part_ml[(j * stride + row) * 2 + 1], g, L);
+    O = fmaf(a.part_o[(j * stride + row) * D + d], g, O);
+  }
+  a.out[row * D + d] = O / L;
+  if (d == 0 && !(__float_as_uint(L) - 1u < 0x7f7fffffu)) atomicOr(a.err, kDevErrSoftmaxDenominator);
+}
+
+hipError_t launch_prefill_combine(hipStream_t st, const PrefillArgs &a, int D) {
+  if (a.splits <= 1) return hipSuccess;
+  hipLaunchKernelGGL(prefill_combine_kernel, dim3((unsigned)((long)a.S * a.Hq)), dim3(D), 0, st, a, D);
+  return hipGetLastError();
+}
 
 hipError_t launch_prefill(hipStream_t st, const PrefillArgs &a, int D) {
   switch (D) {

@@ -154,6 +154,8 @@ __global__ __launch_bounds__(RB *NPB * 64, (QB == 1 || D <= 64) ? 2 : 1) void pr
   int bid = blockIdx.x;
   const int hh = bid % (a.Hkv * HB);
   bid /= (a.Hkv * HB);
+  const int split = bid % a.splits;
+  bid /= a.splits;
   const int qt = a.n_qblocks - 1 - bid;  // longest rows first
   const int h = hh / HB, hb = hh % HB;
   // The wave index is uniform: readfirstlane keeps it (and all that derives
@@ -170,8 +172,21 @@ __global__ __launch_bounds__(RB *NPB * 64, (QB == 1 || D <= 64) ? 2 : 1) void pr
   if (a.causal) key_end = min(key_total, a.P + min(a.S, p0 + WGQ));
   int key_begin = 0;
   if (a.window > 0) key_begin = max(0, a.P + p0 - a.window + 1);
-  const int t_begin = key_begin / BN;
-  const int t_end = (key_end + BN - 1) / BN;
+  int t_begin = key_begin / BN;
+  int t_end = (key_end + BN - 1) / BN;
+  if (a.splits > 1) {  // this split's share of the workgroup's tiles
+    t_begin += split * a.tps;
+    t_end = min(t_end, t_begin + a.tps);
+  }
+  if (t_begin >= t_end) {  // this split sees none of the workgroup's keys (uniform exit)
+    const int pos = wp0 + lane;
+    if (lane < WQ && pos < a.S) {
+      float *ml = a.part_ml + (((long)split * a.S + pos) * a.Hq + head) * 2;
+      ml[0] = -__builtin_inff();
+      ml[1] = 0.0f;
+    }
+    return;
+  }
 
   // Q^T (B operand): lane holds query lq of block qb, dims 16t + 8hl + [0,8).
   bf16x8 qf[QB][DT];
@@ -375,6 +390,29 @@ __global__ __launch_bounds__(RB *NPB * 64, (QB == 1 || D <= 64) ? 2 : 1) void pr
     if (t + 1 < t_end) step(std::integral_constant<int, 1>(), t + 1, sb, sa);
   }
 
+  if (a.splits > 1) {  // unnormalised O and (m, l) of this key split
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const int pos = wp0 + 32 * qb + lq;
+      const float lt = xor32_sum(l[qb]);
+      if (pos < a.S) {
+        const long row = ((long)split * a.S + pos) * a.Hq + head;
+        float *op = a.part_o + row * D + 4 * hl;
+#pragma unroll
+        for (int d = 0; d < DB; ++d)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            *reinterpret_cast<float4 *>(op + d * 32 + 8 * g) =
+                make_float4(oacc[qb][d][4 * g], oacc[qb][d][4 * g + 1], oacc[qb][d][4 * g + 2], oacc[qb][d][4 * g + 3]);
+        if (hl == 0) {
+          a.part_ml[row * 2] = m[qb];
+          a.part_ml[row * 2 + 1] = lt;
+        }
+      }
+    }
+    return;
+  }
+
   // ---- epilogue: O = O^T / l ----
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
@@ -403,7 +441,7 @@ template <int D, int RB, int NPB, int BN, int QB>
 hipError_t launch_shape(hipStream_t st, PrefillArgs a) {
   constexpr int WGQ = NPB * QB * 32;
   a.n_qblocks = (a.S + WGQ - 1) / WGQ;
-  const long blocks = (long)a.n_qblocks * a.Hkv * (a.R / RB);
+  const long blocks = (long)a.n_qblocks * a.splits * a.Hkv * (a.R / RB);
   hipLaunchKernelGGL((prefill_wide_kernel<D, RB, NPB, BN, QB>), dim3((unsigned)blocks), dim3(RB * NPB * 64), 0, st,
                      a);
   return hipGetLastError();
@@ -423,6 +461,7 @@ hipError_t launch_d(hipStream_t st, const PrefillArgs &a) {
 }
 
 }  // namespace
+
 
 hipError_t launch_prefill_wide(hipStream_t st, const PrefillArgs &a, int D) {
   switch (D) {
