@@ -355,29 +355,57 @@ long prefill_base_workgroups(const PrefillArgs &a, int D) {
 // Merges key splits: per (query row, head), M = max m_j, then
 // O = sum_j O_j 2^(m_j - M), L = sum_j l_j 2^(m_j - M), out = O / L. Splits
 // that saw no key of the row (m_j = -inf) contribute nothing. One workgroup of
-// D threads per (row, head); the error bit is set for an invalid L, as the
-// unsplit kernels do (rotary.rs:560-564).
+// D threads per (row, head): the (m, l) pairs of all splits are loaded once
+// into LDS by parallel threads, then every thread accumulates its output
+// element over the splits with independent loads. The error bit is set for an
+// invalid L, as the unsplit kernels do (rotary.rs:560-564).
+constexpr int kMaxPrefillSplits = 256;
+
 __global__ __launch_bounds__(256) void prefill_combine_kernel(const PrefillArgs a, int D) {
+  __shared__ float s_g[kMaxPrefillSplits];  // weight 2^(m_j - M) (0 for empty splits)
+  __shared__ float s_l[kMaxPrefillSplits];
+  __shared__ float s_red[256];
   const long row = blockIdx.x;  // pos * Hq + head
   const int d = threadIdx.x;
   const long stride = (long)a.S * a.Hq;
-  float M = -__builtin_inff();
-  for (int j = 0; j < a.splits; ++j) M = fmaxf(M, a.part_ml[(j * stride + row) * 2]);
-  const float Ms = M == -__builtin_inff() ? 0.0f : M;
-  float L = 0.0f, O = 0.0f;
-  for (int j = 0; j < a.splits; ++j) {
-    const float mj = a.part_ml[(j * stride + row) * 2];
-    if (mj == -__builtin_inff()) continue;
-    const float g = __builtin_amdgcn_exp2f(mj - Ms);
-    L = fmaf(a.part_ml[(j * stride + row) * 2 + 1], g, L);
-    O = fmaf(a.part_o[(j * stride + row) * D + d], g, O);
+  float mj = -__builtin_inff(), lj = 0.0f;
+  for (int j = d; j < a.splits; j += blockDim.x) {  // splits <= kMaxPrefillSplits <= blockDim in practice
+    mj = a.part_ml[(j * stride + row) * 2];
+    lj = a.part_ml[(j * stride + row) * 2 + 1];
   }
+  s_red[d] = mj;
+  __syncthreads();
+  for (int w = blockDim.x / 2; w > 0; w >>= 1) {
+    if (d < w) s_red[d] = fmaxf(s_red[d], s_red[d + w]);
+    __syncthreads();
+  }
+  const float M = s_red[0];
+  const float Ms = M == -__builtin_inff() ? 0.0f : M;
+  if (d < a.splits) {
+    s_g[d] = mj == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(mj - Ms);
+    s_l[d] = lj;
+  }
+  __syncthreads();
+  float L = 0.0f, O = 0.0f;
+  const float *po = a.part_o + row * D + d;
+  int j = 0;
+  for (; j + 4 <= a.splits; j += 4) {  // four independent loads in flight
+    const float o0 = po[(j + 0) * stride * D], o1 = po[(j + 1) * stride * D];
+    const float o2 = po[(j + 2) * stride * D], o3 = po[(j + 3) * stride * D];
+    O = fmaf(o0, s_g[j], O);
+    O = fmaf(o1, s_g[j + 1], O);
+    O = fmaf(o2, s_g[j + 2], O);
+    O = fmaf(o3, s_g[j + 3], O);
+  }
+  for (; j < a.splits; ++j) O = fmaf(po[j * stride * D], s_g[j], O);
+  for (int k = 0; k < a.splits; ++k) L = fmaf(s_l[k], s_g[k], L);
   a.out[row * D + d] = O / L;
   if (d == 0 && !(__float_as_uint(L) - 1u < 0x7f7fffffu)) atomicOr(a.err, kDevErrSoftmaxDenominator);
 }
 
 hipError_t launch_prefill_combine(hipStream_t st, const PrefillArgs &a, int D) {
   if (a.splits <= 1) return hipSuccess;
+  if (a.splits > kMaxPrefillSplits || a.splits > D) return hipErrorInvalidValue;
   hipLaunchKernelGGL(prefill_combine_kernel, dim3((unsigned)((long)a.S * a.Hq)), dim3(D), 0, st, a, D);
   return hipGetLastError();
 }

@@ -97,32 +97,29 @@ __global__ void gemma_prologue_kernel(const float *__restrict__ cos_tab,
 // left untouched.
 // A block owns the 64 buffer positions [P0, P0 + 64), P0 a multiple of 64 (so
 // the slot permutation, which stays inside aligned groups of 16, stays inside
-// the block), of one head. K rows are converted 8 dims per thread with 16-byte
-// loads and stores; V rows go through an LDS tile, from which each thread
-// writes 8 consecutive slots of one V^T row as one 16-byte store.
-// Grid: (blocks over positions, H), 256 threads; D a multiple of 8, <= 256.
+// the block), and 64 dims [d0, d0 + 64) of one head. K rows are converted 8
+// dims per thread with 16-byte loads and stores; V rows go through an LDS
+// tile, from which each thread writes 8 consecutive slots of one V^T row as
+// one 16-byte store.
+// Grid: (blocks over positions, H, D / 64), 256 threads.
 __global__ __launch_bounds__(256) void stage_bf16_kernel(const float *__restrict__ k_rows,
                                                          const float *__restrict__ v_rows, long n, long n_pad,
                                                          int H, int D, bf16 *__restrict__ kb,
                                                          bf16 *__restrict__ vt, long dst_first, long cap) {
   typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
-  // V rows of the block's positions, row stride D + 1 against bank conflicts
-  // (dynamic LDS: 64 * (D + 1) floats).
-  extern __shared__ float tile_mem[];
-  const int TS = D + 1;
-  const int h = blockIdx.y;
+  __shared__ float tile[64][65];  // V[position][dim] of the block, padded against bank conflicts
+  const int h = blockIdx.y, d0 = 64 * blockIdx.z;
   const long P0 = (dst_first & ~63L) + 64L * blockIdx.x;
   const long lo = dst_first, hi = dst_first + n_pad;  // positions this call writes
-  const int chunks = D / 8;
 
   // K rows (and V rows into LDS): position P0 + r holds source row i = P0 + r - dst_first.
-  for (int w = threadIdx.x; w < 64 * chunks; w += 256) {
-    const int r = w / chunks, cc = w % chunks;
+  for (int w = threadIdx.x; w < 64 * 8; w += 256) {
+    const int r = w >> 3, cc = w & 7;
     const long pos = P0 + r, i = pos - dst_first;
     if (pos < lo || pos >= hi) continue;
     float4 k0 = make_float4(0.f, 0.f, 0.f, 0.f), k1 = k0, v0 = k0, v1 = k0;
     if (i < n) {
-      const long base = (i * H + h) * (long)D + 8 * cc;
+      const long base = (i * H + h) * (long)D + d0 + 8 * cc;
       k0 = *reinterpret_cast<const float4 *>(k_rows + base);
       k1 = *reinterpret_cast<const float4 *>(k_rows + base + 4);
       v0 = *reinterpret_cast<const float4 *>(v_rows + base);
@@ -131,29 +128,29 @@ __global__ __launch_bounds__(256) void stage_bf16_kernel(const float *__restrict
     bf16x8 kv;
     kv[0] = (bf16)k0.x; kv[1] = (bf16)k0.y; kv[2] = (bf16)k0.z; kv[3] = (bf16)k0.w;
     kv[4] = (bf16)k1.x; kv[5] = (bf16)k1.y; kv[6] = (bf16)k1.z; kv[7] = (bf16)k1.w;
-    *reinterpret_cast<bf16x8 *>(kb + ((long)h * cap + pos) * D + 8 * cc) = kv;
-    float *t = &tile_mem[r * TS + 8 * cc];
+    *reinterpret_cast<bf16x8 *>(kb + ((long)h * cap + pos) * D + d0 + 8 * cc) = kv;
+    float *t = &tile[r][8 * cc];
     t[0] = v0.x; t[1] = v0.y; t[2] = v0.z; t[3] = v0.w;
     t[4] = v1.x; t[5] = v1.y; t[6] = v1.z; t[7] = v1.w;
   }
   __syncthreads();
 
-  // V^T: row d, slots [P0 + 8c, P0 + 8c + 8); slot s holds the key at
+  // V^T: row d0 + dd, slots [P0 + 8c, P0 + 8c + 8); slot s holds the key at
   // position vt_key_slot(s), which lies in the same aligned 16-group.
-  for (int w = threadIdx.x; w < D * 8; w += 256) {
-    const int d = w / 8, c = w % 8;
+  for (int w = threadIdx.x; w < 64 * 8; w += 256) {
+    const int dd = w >> 3, c = w & 7;
     const long s0 = P0 + 8 * c;
-    bf16 *dst = vt + ((long)h * D + d) * cap;
+    bf16 *dst = vt + ((long)h * D + d0 + dd) * cap;
     const long g0 = s0 & ~15L;  // the aligned 16-group whose keys these slots hold
     if (g0 >= lo && g0 + 16 <= hi) {
       bf16x8 vv;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) vv[j] = (bf16)tile_mem[(vt_key_slot(s0 + j) - P0) * TS + d];
+      for (int j = 0; j < 8; ++j) vv[j] = (bf16)tile[vt_key_slot(s0 + j) - P0][dd];
       *reinterpret_cast<bf16x8 *>(dst + s0) = vv;
     } else {
       for (int j = 0; j < 8; ++j) {
         const long sl = s0 + j, key = vt_key_slot(sl);
-        if (key >= lo && key < hi) dst[sl] = (bf16)tile_mem[(key - P0) * TS + d];
+        if (key >= lo && key < hi) dst[sl] = (bf16)tile[key - P0][dd];
       }
     }
   }
@@ -196,12 +193,11 @@ hipError_t launch_stage_bf16(hipStream_t st, const float *k_rows, const float *v
                              size_t dst_first, size_t dst_cap) {
   long n_pad = (long)n_pad_rows;
   if (n_pad <= 0) return hipSuccess;
-  if ((long)dst_first + n_pad > (long)dst_cap || n_pad < (long)n || D % 8 != 0 || D > 256 || dst_cap % 64 != 0)
+  if ((long)dst_first + n_pad > (long)dst_cap || n_pad < (long)n || D % 64 != 0 || dst_cap % 64 != 0)
     return hipErrorInvalidValue;
   const long first_block = (long)dst_first & ~63L, last = (long)dst_first + n_pad;
-  dim3 grid(blocks_for(last - first_block, 64), (unsigned)H);
-  const size_t lds = 64 * (D + 1) * sizeof(float);
-  hipLaunchKernelGGL(stage_bf16_kernel, grid, dim3(256), lds, st, k_rows, v_rows, (long)n, n_pad,
+  dim3 grid(blocks_for(last - first_block, 64), (unsigned)H, (unsigned)(D / 64));
+  hipLaunchKernelGGL(stage_bf16_kernel, grid, dim3(256), 0, st, k_rows, v_rows, (long)n, n_pad,
                      (int)H, (int)D, kb, vt, (long)dst_first, (long)dst_cap);
   return hipGetLastError();
 }
