@@ -38,10 +38,10 @@ COMMON = [
 ]
 
 
-# Per-source additions. prefill_wide.hip keeps MFMA results in VGPRs: its
-# score accumulators feed VALU code, and the AGPR form round-trips them.
+# Per-source additions. prefill.hip keeps MFMA results in VGPRs: its score
+# accumulators feed VALU code, and the AGPR form round-trips them.
 EXTRA = {
-    "prefill_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

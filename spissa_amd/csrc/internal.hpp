@@ -130,8 +130,6 @@ hipError_t launch_decode(hipStream_t st, const DecodeArgs &a, int D, int RB);
 hipError_t launch_prefill(hipStream_t st, const PrefillArgs &a, int D);
 // Merges the key splits of a split prefill into `out` (and the error flag).
 hipError_t launch_prefill_combine(hipStream_t st, const PrefillArgs &a, int D);
-// head_dim 64 and 128 (prefill_wide.hip); launch_prefill dispatches to it.
-hipError_t launch_prefill_wide(hipStream_t st, const PrefillArgs &a, int D);
 hipError_t launch_generic(hipStream_t st, const GenericArgs &a);
 
 // Keys per split of a decode launch: total_rows = key rows summed over all

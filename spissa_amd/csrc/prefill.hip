@@ -1,25 +1,50 @@
-// prefill.hip -- causal GQA prefill for head_dim 256 (rotary.rs:335-415 with
-// query_len > 1, including chunked prefill against a cache and the
-// sliding-window extension) as a bf16-MFMA flash-attention kernel for gfx950,
-// and the prefill launcher (head_dim 64 and 128 run prefill_wide.hip). Inputs and outputs are
-// f32; Q is rounded to bf16 in registers, K and V are read from bf16 copies
-// (the cache's bf16 shadow for keys already cached, a staging buffer for the
-// rest); scores, softmax state and the output accumulate in f32.
+// prefill.hip -- causal GQA prefill for head_dim 64, 128 and 256
+// (rotary.rs:335-415 with query_len > 1, including chunked prefill against a
+// cache and the sliding-window extension) as a bf16-MFMA flash-attention
+// kernel for gfx950. Inputs and outputs are f32; Q is rounded to bf16 in
+// registers, K and V are read from bf16 copies (the cache's bf16 shadow for
+// tiles below P8, the staging buffer for the rest); scores, softmax state and
+// the output accumulate in f32.
 //
-// Tiling. A workgroup owns NPB blocks of 32 query positions for RB query
-// heads of one KV head (NW = RB*NPB waves, one 32-query block of one head per
-// wave), so every K/V tile staged in LDS serves all RB heads of the group.
-// Per key tile of BN keys a wave computes
-//   S^T = K Q^T   with v_mfma_f32_32x32x16_bf16 (A = K rows from LDS, B = Q in
-//                 registers); the accumulator layout puts one query per lane
-//                 (lane & 31) and 16 of its keys per lane, so the row max and
-//                 sum are lane-local plus one v_permlane32_swap;
-//   O^T += V^T P^T with the same instruction (A = V^T from the transposed LDS
-//                 tile, B = P^T straight from the score registers: the key
-//                 order of the contraction is permuted consistently on both
-//                 operands, so no register shuffle is needed).
-// The online softmax runs in the log2 domain with v_exp_f32.
-// Workgroups are issued longest (last query tile) first for causal balance.
+// Work split. Each wave owns QB 32-query blocks of one query head (QB = 1 in
+// the launched configurations), and the four waves of a workgroup share one KV
+// head: four heads of a group, two heads with two blocks each, or one head
+// with four blocks. Two waves run per SIMD (at most 256 VGPRs each) up to
+// head_dim 128; head_dim 256 runs one wave per SIMD with 32-key tiles.
+// Key splits (PrefillArgs::splits > 1) add workgroups over the key range for
+// grids too small to fill the GPU (short chunks over long caches, few heads);
+// prefill_combine_kernel merges their partial results.
+//
+// Per key tile of BN keys and per query block a wave computes
+//   S^T = K Q^T   v_mfma_f32_32x32x16_bf16, A = K rows from LDS, B = Q^T in
+//                 registers; the accumulator puts one query per lane (lane &
+//                 31) and 16 of its keys per lane, so row max and sum are
+//                 lane-local plus one v_permlane32_swap;
+//   O^T += V^T P^T  A = V^T from LDS, B = P^T straight from the score
+//                 registers (keys of the V^T operand are stored in
+//                 vt_key_slot order, so each lane's 8 keys are 16 contiguous
+//                 bytes).
+// Copies. K and V^T tiles go global -> LDS with global_load_lds_dwordx4 (no
+// staging registers) into two alternating buffers each. The loop is
+// software-pipelined one tile deep: in step t the copies of K(t+2) and V(t+1)
+// are in flight while the exponentials of tile t run on the VALU next to the
+// MFMAs of S(t+1) = K(t+1) Q^T, then O^T += V(t)^T P(t)^T; one barrier per
+// step.
+// Tiles are unpadded; the 16-byte chunks of each row are XOR-swizzled within
+// the row by swz(row), chosen so that the 8 consecutive rows one LDS read
+// serves together (same chunk index) hit 8 distinct 16-byte bank groups:
+//   K tile   [BN keys][D]: chunk c of key row r at byte r*2D  + 16*(c ^ swz(r))
+//   V^T tile [D][BN keys]: chunk c of dim row d at byte d*2BN + 16*(c ^ swz(d))
+// Softmax. The exponent reference m of a row is raised only when the row
+// maximum exceeds it by more than 2^8 (in the log2 domain), so exponentials
+// stay below 256 and the O accumulators are rescaled a handful of times per
+// row instead of on most tiles; O and the sum share m, so O / sum is exact
+// softmax arithmetic.
+// This file is compiled with MFMA results in VGPRs (-amdgpu-mfma-vgpr-form):
+// the score accumulators feed VALU code directly instead of round-tripping
+// through AGPRs.
+#include <type_traits>
+
 #include "internal.hpp"
 
 namespace spissa {
@@ -27,46 +52,109 @@ namespace spissa {
 namespace {
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
-typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
 typedef __attribute__((ext_vector_type(16))) float f32x16;
-typedef __attribute__((ext_vector_type(4))) unsigned u32x4;
-typedef __attribute__((ext_vector_type(2))) unsigned u32x2;
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr float NEG_INF = -__builtin_inff();
+// Largest growth of a row maximum (log2 domain) absorbed without rescaling.
+constexpr float kRescaleSlack = 8.0f;
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// NaN-propagating maximum (v_maximum_f32): no input canonicalisation, and a
+// NaN score reaches the denominator check.
+__device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
 __device__ __forceinline__ float xor32_max(float v) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float xor32_sum(float v) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-__device__ __forceinline__ u32x2 kreg_lo(u32x4 v) { return __builtin_shufflevector(v, v, 0, 1); }
-__device__ __forceinline__ u32x2 kreg_hi(u32x4 v) { return __builtin_shufflevector(v, v, 2, 3); }
+// Copies 16 bytes per lane from src into LDS at lds_base + 16 * lane.
+__device__ __forceinline__ void dma16(const char *src, char *lds_base) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void *)lds_base, 16, 0, 0);
+}
 
-__device__ __forceinline__ bf16x8 cat(bf16x4 a, bf16x4 b) {
-  return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+// Waits for this wave's outstanding global -> LDS copies.
+__device__ __forceinline__ void wait_copies() {
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt and lgkmcnt unconstrained
+}
+
+// XOR swizzle of a row of NC 16-byte chunks (NC = 4, 8, 16 or 32), staying below
+// NC. For a fixed chunk index, any 8 aligned consecutive rows land in 8
+// distinct 16-byte groups modulo 128 bytes and any 16 aligned consecutive rows
+// in 16 distinct groups modulo 256 bytes, so an LDS read is conflict-free
+// whether the hardware serves 8 lanes per 128 bytes or 16 lanes per 256. The
+// swizzle of row 32 b + l does not depend on b.
+template <int NC>
+__device__ __forceinline__ constexpr int swz(int row) {
+  static_assert(NC == 4 || NC == 8 || NC == 16 || NC == 32, "row width");
+  return NC >= 16 ? (row & 15) : NC == 8 ? ((row ^ ((row >> 3) & 1)) & 7) : (((row >> 1) ^ (row >> 2)) & 3);
+}
+
+template <int D, int BN, int NW>
+struct Geom {
+  static constexpr int KBYTES = BN * D * 2;
+  static constexpr int VBYTES = D * BN * 2;
+  static constexpr int KDMA = KBYTES / 1024 / NW;  // K copies per wave per tile
+  static constexpr int VDMA = VBYTES / 1024 / NW;  // V^T copies per wave per tile
+  static constexpr int DT = D / 16;                // 16-dim steps of S^T = K Q^T
+  static constexpr int KB = BN / 32;               // 32-key score blocks
+  static constexpr int KS = BN / 16;               // 16-key steps of O^T += V^T P^T
+  static constexpr int DB = D / 32;                // 32-dim output blocks
+  static constexpr int KNC = D / 8;                // 16-byte chunks per K row
+  static constexpr int VNC = BN / 8;               // 16-byte chunks per V^T row
+  static_assert(KDMA * NW * 1024 == KBYTES && VDMA * NW * 1024 == VBYTES, "tile/wave split");
+};
+
+// S^T of one key tile for the wave's QB query blocks; kbuf is the K tile in LDS.
+template <int D, int BN, int QB>
+__device__ __forceinline__ void score_tile(f32x16 (&s)[QB][BN / 32], const char *kbuf,
+                                           const unsigned (&k_rd)[D / 16],
+                                           const bf16x8 (&qf)[QB][D / 16]) {
+  constexpr int DT = D / 16, KB = BN / 32;
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[qb][kb][i] = 0.0f;
+#pragma unroll
+  for (int tt = 0; tt < DT; ++tt)
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      const bf16x8 kf = *reinterpret_cast<const bf16x8 *>(kbuf + kb * 64 * D + k_rd[tt]);
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb)
+        s[qb][kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[qb][tt], s[qb][kb], 0, 0, 0);
+    }
 }
 
 }  // namespace
 
-// Two waves per SIMD up to head_dim 128; head_dim 256 (O alone is 128
-// accumulators per lane) takes one wave per SIMD with the full register file.
-template <int D, int RB, int NPB, int BN>
-__global__ __launch_bounds__(RB *NPB * 64, D >= 256 ? 1 : 2) void prefill_kernel(const PrefillArgs a) {
+// QB query blocks of 32 per wave (1 or 2); two waves per SIMD unless the
+// accumulators need the whole register file (head_dim 256, or two 128-wide
+// blocks).
+template <int D, int RB, int NPB, int BN, int QB>
+__global__ __launch_bounds__(RB *NPB * 64, ((QB == 1 && D <= 128) || D <= 64) ? 2 : 1) void prefill_kernel(
+    const PrefillArgs a) {
   constexpr int NW = RB * NPB;
-  constexpr int NT = NW * 64;
-  constexpr int KS = D + 8;   // K tile row stride (bf16), padded against LDS bank conflicts
-  constexpr int VS = BN + 4;  // V^T tile row stride (bf16)
-  constexpr int WGQ = NPB * 32;
-  constexpr int DB = D / 32;  // 32-dim output blocks
-  constexpr int KB = BN / 32; // 32-key score blocks
-  constexpr float NEG_INF = -__builtin_inff();
+  constexpr int WQ = QB * 32;  // queries per wave
+  constexpr int WGQ = NPB * WQ;
+  using G = Geom<D, BN, NW>;
+  constexpr int DT = G::DT, KB = G::KB, KS = G::KS, DB = G::DB;
 
-  __shared__ __attribute__((aligned(16))) bf16 Ks[BN * KS];
-  __shared__ __attribute__((aligned(16))) bf16 Vs[D * VS];
+  // Four separate LDS objects (not one array): the compiler then knows that
+  // copies into one buffer do not alias reads of another and does not wait
+  // for the copies before every LDS read.
+  __shared__ __attribute__((aligned(1024))) char k_lds0[G::KBYTES];
+  __shared__ __attribute__((aligned(1024))) char k_lds1[G::KBYTES];
+  __shared__ __attribute__((aligned(1024))) char v_lds0[G::VBYTES];
+  __shared__ __attribute__((aligned(1024))) char v_lds1[G::VBYTES];
 
   const int HB = a.R / RB;
   int bid = blockIdx.x;
@@ -82,11 +170,8 @@ __global__ __launch_bounds__(RB *NPB * 64, D >= 256 ? 1 : 2) void prefill_kernel
   const int r = wave % RB, pb = wave / RB;
   const int head = h * a.R + hb * RB + r;
   const int p0 = qt * WGQ;
-  const int wp0 = p0 + pb * 32;
+  const int wp0 = p0 + pb * WQ;
   const int lq = lane & 31, hl = lane >> 5;
-  const int my_pos = wp0 + lq;
-  const bool pos_ok = my_pos < a.S;
-  const int q_abs = a.P + my_pos;
   const int key_total = a.P + a.S;
 
   int key_end = key_total;
@@ -95,256 +180,304 @@ __global__ __launch_bounds__(RB *NPB * 64, D >= 256 ? 1 : 2) void prefill_kernel
   if (a.window > 0) key_begin = max(0, a.P + p0 - a.window + 1);
   int t_begin = key_begin / BN;
   int t_end = (key_end + BN - 1) / BN;
-  if (a.splits > 1) {  // this split's share of the tiles (empty: m = -inf, l = 0)
+  if (a.splits > 1) {  // this split's share of the workgroup's tiles
     t_begin += split * a.tps;
     t_end = min(t_end, t_begin + a.tps);
   }
+  if (t_begin >= t_end) {  // this split sees none of the workgroup's keys (uniform exit)
+    const int pos = wp0 + lane;
+    if (lane < WQ && pos < a.S) {
+      float *ml = a.part_ml + (((long)split * a.S + pos) * a.Hq + head) * 2;
+      ml[0] = -__builtin_inff();
+      ml[1] = 0.0f;
+    }
+    return;
+  }
 
-  // Q as the B operand of S^T = K Q^T: lane holds query lq, dims 16t + 8hl + [0,8).
-  bf16x8 qf[D / 16];
-  {
-    const int pos = min(my_pos, a.S - 1);
+  // Q^T (B operand): lane holds query lq of block qb, dims 16t + 8hl + [0,8).
+  bf16x8 qf[QB][DT];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const int pos = min(wp0 + 32 * qb + lq, a.S - 1);
     const float *qp = a.q + ((long)pos * a.Hq + head) * D + 8 * hl;
 #pragma unroll
-    for (int t = 0; t < D / 16; ++t) {
+    for (int t = 0; t < DT; ++t) {
       const float4 x0 = *reinterpret_cast<const float4 *>(qp + 16 * t);
       const float4 x1 = *reinterpret_cast<const float4 *>(qp + 16 * t + 4);
       bf16x8 v;
       v[0] = (bf16)x0.x; v[1] = (bf16)x0.y; v[2] = (bf16)x0.z; v[3] = (bf16)x0.w;
       v[4] = (bf16)x1.x; v[5] = (bf16)x1.y; v[6] = (bf16)x1.z; v[7] = (bf16)x1.w;
-      qf[t] = v;
+      qf[qb][t] = v;
     }
   }
+  f32x16 oacc[QB][DB];
+  float m[QB], l[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+#pragma unroll
+    for (int d = 0; d < DB; ++d)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) oacc[qb][d][i] = 0.0f;
+    m[qb] = NEG_INF;
+    l[qb] = 0.0f;
+  }
 
-  f32x16 oacc[DB];
+  // LDS byte offsets of this lane's fragments (key block 0 / dim block 0).
+  // (Rows of a fragment are 32 * block + lq, and 32 * block leaves swz unchanged.)
+  unsigned k_rd[DT], v_rd[KS];
 #pragma unroll
-  for (int d = 0; d < DB; ++d)
+  for (int t = 0; t < DT; ++t) k_rd[t] = lq * 2 * D + 16 * ((2 * t + hl) ^ swz<G::KNC>(lq));
 #pragma unroll
-    for (int i = 0; i < 16; ++i) oacc[d][i] = 0.0f;
-  // Running max m is kept in the scaled log2 domain; scores stay raw and the
-  // scale is folded into the exp2 argument.
-  float m = NEG_INF, l = 0.0f;
+  for (int t = 0; t < KS; ++t) v_rd[t] = lq * 2 * BN + 16 * ((2 * t + hl) ^ swz<G::VNC>(lq));
+
+  // Source of this lane's copies: copy j of the wave fills LDS bytes
+  // [(wave + j*NW) * 1024, +1024) of a tile; lane l writes its 16 bytes at
+  // +16 l, i.e. position p of K row `row` (V^T: dim row d), which holds chunk
+  // p ^ swz(row) of that row. Every source chunk lies inside the tile's row.
+  unsigned k_src[G::KDMA], v_row[G::VDMA], v_col[G::VDMA];
+#pragma unroll
+  for (int j = 0; j < G::KDMA; ++j) {
+    const int byte = (wave + j * NW) * 1024 + lane * 16;
+    const int row = byte / (2 * D), p = (byte % (2 * D)) / 16;
+    k_src[j] = (unsigned)(row * D + 8 * (p ^ swz<G::KNC>(row))) * 2u;
+  }
+#pragma unroll
+  for (int j = 0; j < G::VDMA; ++j) {
+    const int byte = (wave + j * NW) * 1024 + lane * 16;
+    const int d = byte / (2 * BN), p = (byte % (2 * BN)) / 16;
+    v_row[j] = d;
+    v_col[j] = 8 * (p ^ swz<G::VNC>(d));
+  }
+  const char *kb_c = reinterpret_cast<const char *>(a.kb_cache + (long)h * a.cap_cache * D);
+  const char *kb_s = reinterpret_cast<const char *>(a.kb_stage + (long)h * a.cap_stage * D);
+  const char *vt_c = reinterpret_cast<const char *>(a.vt_cache + (long)h * D * a.cap_cache);
+  const char *vt_s = reinterpret_cast<const char *>(a.vt_stage + (long)h * D * a.cap_stage);
+
+  // Tiles below P8 come from the cache shadow, the others from staging (P8 is
+  // a multiple of the tile width, so the choice is uniform per tile).
+  auto copy_k = [&](int t, char *dst) {
+    const int nk = t * BN;
+    const char *src = nk < a.P8 ? kb_c + (long)nk * D * 2 : kb_s + (long)(nk - a.P8) * D * 2;
+#pragma unroll
+    for (int j = 0; j < G::KDMA; ++j) dma16(src + k_src[j], dst + (wave + j * NW) * 1024);
+  };
+  auto copy_v = [&](int t, char *dst) {
+    const int nk = t * BN;
+    const bool cached = nk < a.P8;
+    const char *src = cached ? vt_c + (long)nk * 2 : vt_s + (long)(nk - a.P8) * 2;
+    const unsigned stride = (unsigned)(cached ? a.cap_cache : a.cap_stage);
+#pragma unroll
+    for (int j = 0; j < G::VDMA; ++j) dma16(src + (v_row[j] * stride + v_col[j]) * 2u, dst + (wave + j * NW) * 1024);
+  };
+
+  // Visible keys [vis_lo, vis_hi] of this lane's two queries.
+  int vis_lo[QB], vis_hi[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const int q_abs = a.P + wp0 + 32 * qb + lq;
+    vis_hi[qb] = a.causal ? min(q_abs, key_total - 1) : key_total - 1;
+    vis_lo[qb] = a.window > 0 ? q_abs - a.window + 1 : 0;
+  }
+  const int wave_min_q = a.P + wp0;
+  const int wave_max_q = a.P + min(wp0 + WQ - 1, a.S - 1);
   const float c = a.qk_scale_log2;
 
-  const int wave_min_q = a.P + wp0;
-  const int wave_max_q = a.P + min(wp0 + 31, a.S - 1);
-  const bool wave_live = wp0 < a.S;
-
-  // Per-thread staging slots, fixed for the whole loop: K chunk (row, 8 dims)
-  // and V^T chunk (dim, 8 keys) offsets inside a tile and inside LDS.
-  constexpr int KCH = BN * (D / 8) / NT;  // 16-byte K chunks per thread per tile
-  constexpr int VCH = D * (BN / 8) / NT;  // 16-byte V^T chunks per thread per tile
-  static_assert(KCH * NT == BN * (D / 8) && VCH * NT == D * (BN / 8), "tile/thread mismatch");
-  int k_row[KCH], k_lds[KCH], v_dim[VCH], v_kc[VCH], v_lds[VCH];
-#pragma unroll
-  for (int u = 0; u < KCH; ++u) {
-    const int cc = threadIdx.x + u * NT;
-    k_row[u] = cc / (D / 8);
-    const int col = (cc % (D / 8)) * 8;
-    k_lds[u] = k_row[u] * KS + col;
-    k_row[u] = k_row[u] * D + col;  // element offset of the chunk inside a tile of D-wide rows
-  }
-#pragma unroll
-  for (int u = 0; u < VCH; ++u) {
-    const int cc = threadIdx.x + u * NT;
-    v_dim[u] = cc / (BN / 8);
-    v_kc[u] = (cc % (BN / 8)) * 8;
-    v_lds[u] = v_dim[u] * VS + v_kc[u];
-  }
-  const bf16 *kb_c = a.kb_cache + (long)h * a.cap_cache * D;
-  const bf16 *kb_s = a.kb_stage + (long)h * a.cap_stage * D;
-  const bf16 *vt_c = a.vt_cache + (long)h * D * a.cap_cache;
-  const bf16 *vt_s = a.vt_stage + (long)h * D * a.cap_stage;
-
-  // The next tile's K / V^T chunks are loaded into registers while the
-  // current tile is computed (register double buffering). Tiles never straddle
-  // the cache / staging boundary P8 (a multiple of the tile width), so the
-  // source buffer is a uniform choice per tile. Iteration t_begin - 1 only
-  // loads the first tile.
-  u32x4 kreg[KCH], vreg[VCH];
-  for (int t = t_begin - 1; t < t_end; ++t) {
+  // One pipelined step on tile t with scores in `cur`: copies of K(t+2) and
+  // V(t+1); mask and softmax of tile t; S(t+1) into `nxt` (also on the last
+  // tile, where it reads a stale buffer and is never used: keeping it
+  // unconditional lets its MFMAs interleave with the softmax VALU work);
+  // O^T += V(t)^T P(t)^T. O selects the buffers.
+  auto step = [&](auto O_, int t, f32x16 (&cur)[QB][KB], f32x16 (&nxt)[QB][KB]) {
+    constexpr int O = decltype(O_)::value;
+    char *const k_this = O ? k_lds1 : k_lds0;  // receives K(t+2)
+    char *const k_next = O ? k_lds0 : k_lds1;  // holds K(t+1)
+    char *const v_this = O ? v_lds1 : v_lds0;  // holds V(t)
+    char *const v_next = O ? v_lds0 : v_lds1;  // receives V(t+1)
+    if (t + 2 < t_end) copy_k(t + 2, k_this);
+    if (t + 1 < t_end) copy_v(t + 1, v_next);
     const int kt0 = t * BN;
-    if (t >= t_begin) {
-      __syncthreads();  // every wave is done with the previous tile
-#pragma unroll
-      for (int u = 0; u < KCH; ++u) *reinterpret_cast<u32x4 *>(&Ks[k_lds[u]]) = kreg[u];
-#pragma unroll
-      for (int u = 0; u < VCH; ++u) {
-        *reinterpret_cast<u32x2 *>(&Vs[v_lds[u]]) = kreg_lo(vreg[u]);
-        *reinterpret_cast<u32x2 *>(&Vs[v_lds[u] + 4]) = kreg_hi(vreg[u]);
-      }
-      __syncthreads();
-    }
-    if (t + 1 < t_end) {
-      const int nk = kt0 + BN;
-      const bool from_cache = nk < a.P8;
-      const bf16 *kt = from_cache ? kb_c + (long)nk * D : kb_s + (long)(nk - a.P8) * D;
-      const bf16 *vt = from_cache ? vt_c + nk : vt_s + (nk - a.P8);
-      const long vstride = from_cache ? a.cap_cache : a.cap_stage;
-#pragma unroll
-      for (int u = 0; u < KCH; ++u) kreg[u] = *reinterpret_cast<const u32x4 *>(kt + k_row[u]);
-#pragma unroll
-      for (int u = 0; u < VCH; ++u)
-        vreg[u] = *reinterpret_cast<const u32x4 *>(vt + (long)v_dim[u] * vstride + v_kc[u]);
-    }
-    if (t < t_begin) continue;
 
-    const bool active = wave_live && !(a.causal && kt0 > wave_max_q) &&
-                        !(a.window > 0 && kt0 + BN - 1 + a.window <= wave_min_q);
-    if (!active) continue;
-
-    // ---- S^T = K Q^T (raw scores) ----
-    f32x16 sacc[KB];
+    // Masked keys become -inf in a copy of the scores.
+    float sc[QB][KB][16];
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) {
+    for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) sacc[kb][i] = 0.0f;
+      for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-      for (int tt = 0; tt < D / 16; ++tt) {
-        const bf16x8 ka =
-            *reinterpret_cast<const bf16x8 *>(&Ks[(kb * 32 + lq) * KS + 16 * tt + 8 * hl]);
-        sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[tt], sacc[kb], 0, 0, 0);
-      }
-    }
-
-    // ---- mask (diagonal and tail tiles only), tile max ----
+        for (int i = 0; i < 16; ++i) sc[qb][kb][i] = cur[qb][kb][i];
     const bool need_mask = (a.causal && kt0 + BN - 1 > wave_min_q) ||
-                           (a.window > 0 && kt0 + a.window <= wave_max_q) ||
-                           (kt0 + BN > key_total);
-    // Masked scores go to a copy: writing -inf in place into the MFMA
-    // accumulator registers gave wrong results on masked tiles.
-    float sc[KB][16];
+                           (a.window > 0 && kt0 + a.window <= wave_max_q) || (kt0 + BN > key_total);
+    if (need_mask) {
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb)
+      for (int qb = 0; qb < QB; ++qb) {
+        const int lo = vis_lo[qb] - kt0 - 4 * hl, hi = vis_hi[qb] - kt0 - 4 * hl;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float v = sacc[kb][i];
-        if (need_mask) {
-          const int key = kt0 + kb * 32 + 8 * (i >> 2) + 4 * hl + (i & 3);
-          const bool masked = (a.causal && key > q_abs) ||
-                              (a.window > 0 && key + a.window <= q_abs) || key >= key_total;
-          if (masked) v = NEG_INF;
-        }
-        sc[kb][i] = v;
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int kk = kb * 32 + 8 * (i >> 2) + (i & 3);
+            sc[qb][kb][i] = (kk < lo || kk > hi) ? NEG_INF : sc[qb][kb][i];
+          }
       }
-    float tmax = NEG_INF;
-#pragma unroll
-    for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-      for (int i = 0; i < 16; i += 2) tmax = fmaxf(tmax, fmaxf(sc[kb][i], sc[kb][i + 1]));
-    tmax = xor32_max(tmax) * c;
-
-    // ---- online softmax; rescale O only when some row's maximum grew ----
-    const float mnew = fmaxf(m, tmax);
-    const float ms = mnew == NEG_INF ? 0.0f : mnew;
-    if (__ballot(mnew > m)) {
-      const float alpha = fast_exp2(m - ms);
-      l *= alpha;
-#pragma unroll
-      for (int d = 0; d < DB; ++d)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) oacc[d][i] *= alpha;
     }
-    m = mnew;
 
-    // ---- O^T += V^T P^T ----
+    // Softmax of tile t, part 1: row maxima, exponent references, and the
+    // (rare) rescale of O.
+    float alpha[QB], ms[QB];
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) {
-      bf16x8 pa, pb;
-      float ls = 0.0f;
+    for (int qb = 0; qb < QB; ++qb) {
+      float mx = sc[qb][0][0];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float p0v = fast_exp2(fmaf(sc[kb][i], c, -ms));
-        const float p1v = fast_exp2(fmaf(sc[kb][i + 8], c, -ms));
-        ls += p0v + p1v;
-        pa[i] = (bf16)p0v;
-        pb[i] = (bf16)p1v;
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = vmax(mx, sc[qb][kb][i]);
+      mx = xor32_max(mx) * c;
+      const bool raise = mx > m[qb] + kRescaleSlack;
+      const float mnew = raise ? mx : m[qb];
+      ms[qb] = mnew == NEG_INF ? 0.0f : mnew;
+      alpha[qb] = fast_exp2(m[qb] - ms[qb]);
+      m[qb] = mnew;
+      if (__ballot(raise)) {
+#pragma unroll
+        for (int d = 0; d < DB; ++d)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) oacc[qb][d][i] *= alpha[qb];
       }
-      l += ls;
+    }
+
+    // Part 2: probabilities (bf16 B operand of PV) on the VALU; the MFMAs of
+    // S(t+1) that follow are independent of them and overlap.
+    float psum[QB];
+    bf16x8 pf[QB][KS];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      psum[qb] = 0.0f;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        bf16x8 p;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float pv = fast_exp2(fmaf(sc[qb][ks >> 1][8 * (ks & 1) + j], c, -ms[qb]));
+          psum[qb] += pv;
+          p[j] = (bf16)pv;
+        }
+        pf[qb][ks] = p;
+      }
+    }
+    score_tile<D, BN, QB>(nxt, k_next, k_rd, qf);
+
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) l[qb] = l[qb] * alpha[qb] + psum[qb];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
       for (int d = 0; d < DB; ++d) {
-        // V^T rows hold keys in vt_key_slot order: this lane's 8 keys of each
-        // 16-key step are contiguous.
-        const bf16 *vrow = &Vs[(d * 32 + lq) * VS + kb * 32 + 8 * hl];
-        const bf16x8 va = cat(*reinterpret_cast<const bf16x4 *>(vrow),
-                              *reinterpret_cast<const bf16x4 *>(vrow + 4));
-        oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pa, oacc[d], 0, 0, 0);
-        const bf16x8 vb = cat(*reinterpret_cast<const bf16x4 *>(vrow + 16),
-                              *reinterpret_cast<const bf16x4 *>(vrow + 20));
-        oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vb, pb, oacc[d], 0, 0, 0);
+        const bf16x8 vf = *reinterpret_cast<const bf16x8 *>(v_this + d * 64 * BN + v_rd[ks]);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb)
+          oacc[qb][d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[qb][ks], oacc[qb][d], 0, 0, 0);
       }
-    }
+    wait_copies();
+    __syncthreads();
+  };
+
+  // Prologue: K(t0), V(t0), K(t0+1) copied; S(t0) computed.
+  f32x16 sa[QB][KB], sb[QB][KB];
+  copy_k(t_begin, k_lds0);
+  copy_v(t_begin, v_lds0);
+  if (t_begin + 1 < t_end) copy_k(t_begin + 1, k_lds1);
+  wait_copies();
+  __syncthreads();
+  score_tile<D, BN, QB>(sa, k_lds0, k_rd, qf);
+  __syncthreads();  // every wave is done with K(t0) before K(t0+2) lands in its buffer
+
+  for (int t = t_begin; t < t_end; t += 2) {
+    step(std::integral_constant<int, 0>(), t, sa, sb);
+    if (t + 1 < t_end) step(std::integral_constant<int, 1>(), t + 1, sb, sa);
   }
 
-  const float lt = xor32_sum(l);
   if (a.splits > 1) {  // unnormalised O and (m, l) of this key split
-    if (pos_ok) {
-      const long row = ((long)split * a.S + my_pos) * a.Hq + head;
-      float *op = a.part_o + row * D + 4 * hl;
 #pragma unroll
-      for (int d = 0; d < DB; ++d)
+    for (int qb = 0; qb < QB; ++qb) {
+      const int pos = wp0 + 32 * qb + lq;
+      const float lt = xor32_sum(l[qb]);
+      if (pos < a.S) {
+        const long row = ((long)split * a.S + pos) * a.Hq + head;
+        float *op = a.part_o + row * D + 4 * hl;
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
-          *reinterpret_cast<float4 *>(op + d * 32 + 8 * g) =
-              make_float4(oacc[d][4 * g], oacc[d][4 * g + 1], oacc[d][4 * g + 2], oacc[d][4 * g + 3]);
-      if (hl == 0) {
-        a.part_ml[row * 2] = m;
-        a.part_ml[row * 2 + 1] = lt;
+        for (int d = 0; d < DB; ++d)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            *reinterpret_cast<float4 *>(op + d * 32 + 8 * g) =
+                make_float4(oacc[qb][d][4 * g], oacc[qb][d][4 * g + 1], oacc[qb][d][4 * g + 2], oacc[qb][d][4 * g + 3]);
+        if (hl == 0) {
+          a.part_ml[row * 2] = m[qb];
+          a.part_ml[row * 2 + 1] = lt;
+        }
       }
     }
     return;
   }
 
   // ---- epilogue: O = O^T / l ----
-  if (pos_ok) {
-    if (hl == 0 && !(lt > 0.0f && lt < __builtin_inff())) atomicOr(a.err, kDevErrSoftmaxDenominator);
-    const float inv = 1.0f / lt;
-    float *op = a.out + ((long)my_pos * a.Hq + head) * D + 4 * hl;
 #pragma unroll
-    for (int d = 0; d < DB; ++d) {
+  for (int qb = 0; qb < QB; ++qb) {
+    const int pos = wp0 + 32 * qb + lq;
+    const float lt = xor32_sum(l[qb]);
+    if (pos < a.S) {
+      // positive, finite and non-zero, tested on the bits (NaN fails it)
+      if (hl == 0 && !(__float_as_uint(lt) - 1u < 0x7f7fffffu)) atomicOr(a.err, kDevErrSoftmaxDenominator);
+      const float inv = 1.0f / lt;
+      float *op = a.out + ((long)pos * a.Hq + head) * D + 4 * hl;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        float4 v = make_float4(oacc[d][4 * g] * inv, oacc[d][4 * g + 1] * inv,
-                               oacc[d][4 * g + 2] * inv, oacc[d][4 * g + 3] * inv);
-        *reinterpret_cast<float4 *>(op + d * 32 + 8 * g) = v;
-      }
+      for (int d = 0; d < DB; ++d)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float4 v = make_float4(oacc[qb][d][4 * g] * inv, oacc[qb][d][4 * g + 1] * inv,
+                                 oacc[qb][d][4 * g + 2] * inv, oacc[qb][d][4 * g + 3] * inv);
+          *reinterpret_cast<float4 *>(op + d * 32 + 8 * g) = v;
+        }
     }
   }
 }
 
 namespace {
 
-template <int D, int RB, int NPB>
-hipError_t launch_cfg(hipStream_t st, PrefillArgs a) {
-  constexpr int BN = D >= 256 ? 32 : 64;
-  constexpr int WGQ = NPB * 32;
+template <int D, int RB, int NPB, int BN, int QB>
+hipError_t launch_shape(hipStream_t st, PrefillArgs a) {
+  constexpr int WGQ = NPB * QB * 32;
   a.n_qblocks = (a.S + WGQ - 1) / WGQ;
   const long blocks = (long)a.n_qblocks * a.splits * a.Hkv * (a.R / RB);
-  hipLaunchKernelGGL((prefill_kernel<D, RB, NPB, BN>), dim3((unsigned)blocks), dim3(RB * NPB * 64),
-                     0, st, a);
+  hipLaunchKernelGGL((prefill_kernel<D, RB, NPB, BN, QB>), dim3((unsigned)blocks), dim3(RB * NPB * 64), 0, st,
+                     a);
   return hipGetLastError();
 }
 
-// Four waves per workgroup (one per SIMD): four query heads of a KV group
-// with one 32-position block, two heads with two blocks, or one head with four
-// blocks (also for groups of three or five heads).
+// Four-wave workgroups, 32 queries per wave, 64-key tiles (32 at head_dim
+// 256), two waves per SIMD (one at head_dim 256): four heads of the KV group,
+// two heads with two blocks, or one head with four blocks. (64 queries per
+// wave halves the LDS fragment reads per
+// MFMA but, at head_dim 128, needs more than 256 VGPRs and measured slower;
+// at head_dim 64 it halves the workgroup count, which a 2048-token prefill
+// cannot afford.)
 template <int D>
 hipError_t launch_d(hipStream_t st, const PrefillArgs &a) {
-  if (a.R % 4 == 0) return launch_cfg<D, 4, 1>(st, a);
-  if (a.R % 2 == 0) return launch_cfg<D, 2, 2>(st, a);
-  return launch_cfg<D, 1, 4>(st, a);
+  constexpr int BN = D >= 256 ? 32 : 64;  // head_dim 256: 32-key tiles, one wave per SIMD
+  if (a.R % 4 == 0) return launch_shape<D, 4, 1, BN, 1>(st, a);
+  if (a.R % 2 == 0) return launch_shape<D, 2, 2, BN, 1>(st, a);
+  return launch_shape<D, 1, 4, BN, 1>(st, a);
 }
 
 }  // namespace
 
+
 bool prefill_supported(int D) { return D == 64 || D == 128 || D == 256; }
 
-// Both kernels launch four-wave workgroups of 32 queries per wave: four heads
-// x 32 queries, two heads x 64, or one head x 128 (launch_d here and in
-// prefill_wide.hip).
+// Four-wave workgroups of 32 queries per wave: four heads x 32 queries, two
+// heads x 64, or one head x 128 (launch_d above).
 int prefill_wg_queries(const PrefillArgs &a, int) { return a.R % 4 == 0 ? 32 : a.R % 2 == 0 ? 64 : 128; }
 int prefill_wgs_per_cu(int D) { return D >= 256 ? 1 : 2; }
-int prefill_tile_keys(int D) { return D >= 256 ? 32 : 64; }
+int prefill_tile_keys(int D) { return D >= 256 ? 32 : 64; }  // BN of launch_d
 
 long prefill_base_workgroups(const PrefillArgs &a, int D) {
   const int wgq = prefill_wg_queries(a, D);
@@ -412,8 +545,8 @@ hipError_t launch_prefill_combine(hipStream_t st, const PrefillArgs &a, int D) {
 
 hipError_t launch_prefill(hipStream_t st, const PrefillArgs &a, int D) {
   switch (D) {
-    case 64:
-    case 128: return launch_prefill_wide(st, a, D);
+    case 64: return launch_d<64>(st, a);
+    case 128: return launch_d<128>(st, a);
     case 256: return launch_d<256>(st, a);
     default: return hipErrorInvalidValue;
   }
