@@ -26,18 +26,26 @@
 //                 bytes).
 // Copies. K and V^T tiles go global -> LDS with global_load_lds_dwordx4 (no
 // staging registers) into two alternating buffers each. The loop is
-// software-pipelined one tile deep: in step t the copies of K(t+2) and V(t+1)
-// are in flight while the exponentials of tile t run on the VALU next to the
-// MFMAs of S(t+1) = K(t+1) Q^T, then O^T += V(t)^T P(t)^T; one barrier per
-// step.
+// software-pipelined one tile deep. In step t the copies of K(t+2) and V(t+1)
+// are in flight while
+//   part A: the exponentials of tile t run on the VALU next to the MFMAs of
+//           S(t+1) = K(t+1) Q^T;
+//   part B: O^T += V(t)^T P(t)^T runs on the MFMAs next to the row maxima of
+//           tile t+1, which fix the exponent reference of step t+1;
+// then the (rare) rescale of O and one barrier. Both parts are one basic
+// block, so the compiler interleaves them freely.
+// Masks. The score accumulators of a masked tile (causal diagonal, window
+// edge, keys past the end) start at -inf for the hidden keys instead of 0,
+// so the MFMAs yield -inf there and the maxima and exponentials need no
+// per-element selects; unmasked tiles start from an inline zero.
 // Tiles are unpadded; the 16-byte chunks of each row are XOR-swizzled within
 // the row by swz(row), chosen so that the 8 consecutive rows one LDS read
 // serves together (same chunk index) hit 8 distinct 16-byte bank groups:
 //   K tile   [BN keys][D]: chunk c of key row r at byte r*2D  + 16*(c ^ swz(r))
 //   V^T tile [D][BN keys]: chunk c of dim row d at byte d*2BN + 16*(c ^ swz(d))
 // Softmax. The exponent reference m of a row is raised only when the row
-// maximum exceeds it by more than 2^8 (in the log2 domain), so exponentials
-// stay below 256 and the O accumulators are rescaled a handful of times per
+// maximum exceeds it by more than 8 (log2 domain), so exponentials stay
+// below 256 and the O accumulators are rescaled a handful of times per
 // row instead of on most tiles; O and the sum share m, so O / sum is exact
 // softmax arithmetic.
 // This file is compiled with MFMA results in VGPRs (-amdgpu-mfma-vgpr-form):
@@ -111,26 +119,24 @@ struct Geom {
   static_assert(KDMA * NW * 1024 == KBYTES && VDMA * NW * 1024 == VBYTES, "tile/wave split");
 };
 
-// S^T of one key tile for the wave's QB query blocks; kbuf is the K tile in LDS.
-template <int D, int BN, int QB>
+// S^T of one key tile for the wave's QB query blocks over the 16-dim steps
+// [T0, T1): the first step starts from zero (ZERO) or from s (the mask bias),
+// later ones accumulate; kbuf is the K tile in LDS.
+template <int D, int BN, int QB, int T0, int T1, bool ZERO>
 __device__ __forceinline__ void score_tile(f32x16 (&s)[QB][BN / 32], const char *kbuf,
                                            const unsigned (&k_rd)[D / 16],
                                            const bf16x8 (&qf)[QB][D / 16]) {
-  constexpr int DT = D / 16, KB = BN / 32;
+  constexpr int KB = BN / 32;
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-    for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s[qb][kb][i] = 0.0f;
-#pragma unroll
-  for (int tt = 0; tt < DT; ++tt)
+  for (int tt = T0; tt < T1; ++tt)
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
       const bf16x8 kf = *reinterpret_cast<const bf16x8 *>(kbuf + kb * 64 * D + k_rd[tt]);
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb)
-        s[qb][kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[qb][tt], s[qb][kb], 0, 0, 0);
+      for (int qb = 0; qb < QB; ++qb) {
+        const f32x16 acc = (ZERO && tt == T0) ? f32x16{} : s[qb][kb];
+        s[qb][kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[qb][tt], acc, 0, 0, 0);
+      }
     }
 }
 
@@ -234,20 +240,18 @@ __global__ __launch_bounds__(RB *NPB * 64, ((QB == 1 && D <= 128) || D <= 64) ? 
   // [(wave + j*NW) * 1024, +1024) of a tile; lane l writes its 16 bytes at
   // +16 l, i.e. position p of K row `row` (V^T: dim row d), which holds chunk
   // p ^ swz(row) of that row. Every source chunk lies inside the tile's row.
-  unsigned k_src[G::KDMA], v_row[G::VDMA], v_col[G::VDMA];
-#pragma unroll
-  for (int j = 0; j < G::KDMA; ++j) {
+  // The offsets are recomputed per copy (a few VALU operations) rather than
+  // held in registers across the loop.
+  auto k_src = [&](int j) {
     const int byte = (wave + j * NW) * 1024 + lane * 16;
     const int row = byte / (2 * D), p = (byte % (2 * D)) / 16;
-    k_src[j] = (unsigned)(row * D + 8 * (p ^ swz<G::KNC>(row))) * 2u;
-  }
-#pragma unroll
-  for (int j = 0; j < G::VDMA; ++j) {
+    return (unsigned)(row * D + 8 * (p ^ swz<G::KNC>(row))) * 2u;
+  };
+  auto v_src = [&](int j, unsigned stride) {
     const int byte = (wave + j * NW) * 1024 + lane * 16;
     const int d = byte / (2 * BN), p = (byte % (2 * BN)) / 16;
-    v_row[j] = d;
-    v_col[j] = 8 * (p ^ swz<G::VNC>(d));
-  }
+    return ((unsigned)d * stride + (unsigned)(8 * (p ^ swz<G::VNC>(d)))) * 2u;
+  };
   const char *kb_c = reinterpret_cast<const char *>(a.kb_cache + (long)h * a.cap_cache * D);
   const char *kb_s = reinterpret_cast<const char *>(a.kb_stage + (long)h * a.cap_stage * D);
   const char *vt_c = reinterpret_cast<const char *>(a.vt_cache + (long)h * D * a.cap_cache);
@@ -259,7 +263,7 @@ __global__ __launch_bounds__(RB *NPB * 64, ((QB == 1 && D <= 128) || D <= 64) ? 
     const int nk = t * BN;
     const char *src = nk < a.P8 ? kb_c + (long)nk * D * 2 : kb_s + (long)(nk - a.P8) * D * 2;
 #pragma unroll
-    for (int j = 0; j < G::KDMA; ++j) dma16(src + k_src[j], dst + (wave + j * NW) * 1024);
+    for (int j = 0; j < G::KDMA; ++j) dma16(src + k_src(j), dst + (wave + j * NW) * 1024);
   };
   auto copy_v = [&](int t, char *dst) {
     const int nk = t * BN;
@@ -267,7 +271,7 @@ __global__ __launch_bounds__(RB *NPB * 64, ((QB == 1 && D <= 128) || D <= 64) ? 
     const char *src = cached ? vt_c + (long)nk * 2 : vt_s + (long)(nk - a.P8) * 2;
     const unsigned stride = (unsigned)(cached ? a.cap_cache : a.cap_stage);
 #pragma unroll
-    for (int j = 0; j < G::VDMA; ++j) dma16(src + (v_row[j] * stride + v_col[j]) * 2u, dst + (wave + j * NW) * 1024);
+    for (int j = 0; j < G::VDMA; ++j) dma16(src + v_src(j, stride), dst + (wave + j * NW) * 1024);
   };
 
   // Visible keys [vis_lo, vis_hi] of this lane's two queries.
@@ -282,32 +286,23 @@ __global__ __launch_bounds__(RB *NPB * 64, ((QB == 1 && D <= 128) || D <= 64) ? 
   const int wave_max_q = a.P + min(wp0 + WQ - 1, a.S - 1);
   const float c = a.qk_scale_log2;
 
-  // One pipelined step on tile t with scores in `cur`: copies of K(t+2) and
-  // V(t+1); mask and softmax of tile t; S(t+1) into `nxt` (also on the last
-  // tile, where it reads a stale buffer and is never used: keeping it
-  // unconditional lets its MFMAs interleave with the softmax VALU work);
-  // O^T += V(t)^T P(t)^T. O selects the buffers.
-  auto step = [&](auto O_, int t, f32x16 (&cur)[QB][KB], f32x16 (&nxt)[QB][KB]) {
-    constexpr int O = decltype(O_)::value;
-    char *const k_this = O ? k_lds1 : k_lds0;  // receives K(t+2)
-    char *const k_next = O ? k_lds0 : k_lds1;  // holds K(t+1)
-    char *const v_this = O ? v_lds1 : v_lds0;  // holds V(t)
-    char *const v_next = O ? v_lds0 : v_lds1;  // receives V(t+1)
-    if (t + 2 < t_end) copy_k(t + 2, k_this);
-    if (t + 1 < t_end) copy_v(t + 1, v_next);
+  // Whether tile t needs a mask (uniform): the causal diagonal, the window's
+  // lower edge, or keys past the end.
+  auto tile_masked = [&](int t) {
     const int kt0 = t * BN;
-
-    // Masked keys become -inf in a copy of the scores.
-    float sc[QB][KB][16];
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) sc[qb][kb][i] = cur[qb][kb][i];
-    const bool need_mask = (a.causal && kt0 + BN - 1 > wave_min_q) ||
-                           (a.window > 0 && kt0 + a.window <= wave_max_q) || (kt0 + BN > key_total);
-    if (need_mask) {
+    return (a.causal && kt0 + BN - 1 > wave_min_q) || (a.window > 0 && kt0 + a.window <= wave_max_q) ||
+           (kt0 + BN > key_total);
+  };
+  // Masking: the score accumulators of a masked tile start at -inf for the
+  // keys a row does not see (0 elsewhere), so the MFMAs produce -inf there
+  // and the maxima and exponentials need no selects; unmasked tiles start
+  // from an inline zero. Score element i of block kb is key
+  // kb*32 + 8(i/4) + 4hl + i%4 of its tile. (Keys beyond the last one are zero
+  // padding, so -inf + finite stays -inf.) This issues the first 16-dim step
+  // of S(t); score_tile<..., 1, DT, false> adds the rest.
+  auto score_first = [&](f32x16 (&s)[QB][KB], const char *kbuf, int t) {
+    if (tile_masked(t)) {
+      const int kt0 = t * BN;
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
         const int lo = vis_lo[qb] - kt0 - 4 * hl, hi = vis_hi[qb] - kt0 - 4 * hl;
@@ -316,58 +311,76 @@ __global__ __launch_bounds__(RB *NPB * 64, ((QB == 1 && D <= 128) || D <= 64) ? 
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             const int kk = kb * 32 + 8 * (i >> 2) + (i & 3);
-            sc[qb][kb][i] = (kk < lo || kk > hi) ? NEG_INF : sc[qb][kb][i];
+            s[qb][kb][i] = (kk < lo || kk > hi) ? NEG_INF : 0.0f;
           }
       }
+      score_tile<D, BN, QB, 0, 1, false>(s, kbuf, k_rd, qf);
+    } else {
+      score_tile<D, BN, QB, 0, 1, true>(s, kbuf, k_rd, qf);
     }
-
-    // Softmax of tile t, part 1: row maxima, exponent references, and the
-    // (rare) rescale of O.
-    float alpha[QB], ms[QB];
+  };
+  // Row maxima of a score tile (log2 domain).
+  auto row_max = [&](const f32x16 (&s)[QB][KB], float (&mx)[QB]) {
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-      float mx = sc[qb][0][0];
+      float v = s[qb][0][0];
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) mx = vmax(mx, sc[qb][kb][i]);
-      mx = xor32_max(mx) * c;
-      const bool raise = mx > m[qb] + kRescaleSlack;
-      const float mnew = raise ? mx : m[qb];
-      ms[qb] = mnew == NEG_INF ? 0.0f : mnew;
-      alpha[qb] = fast_exp2(m[qb] - ms[qb]);
-      m[qb] = mnew;
-      if (__ballot(raise)) {
-#pragma unroll
-        for (int d = 0; d < DB; ++d)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) oacc[qb][d][i] *= alpha[qb];
-      }
+        for (int i = 0; i < 16; ++i) v = vmax(v, s[qb][kb][i]);
+      mx[qb] = xor32_max(v) * c;
     }
+  };
 
-    // Part 2: probabilities (bf16 B operand of PV) on the VALU; the MFMAs of
-    // S(t+1) that follow are independent of them and overlap.
+  // Exponent reference per row: exponentials of a tile are taken against ms
+  // (m, or 0 while m = -inf); m rises only by more than kRescaleSlack.
+  float ms[QB];
+
+  // One pipelined step on tile t (scores in `cur`, exponent reference ms
+  // already covering tile t, O and l already scaled to it):
+  //   copies of K(t+2) and V(t+1) go out;
+  //   part A: the probabilities of tile t on the VALU next to the MFMAs of
+  //     S(t+1) = K(t+1) Q^T (unconditional: on the last tile it reads a
+  //     stale buffer and its result is ignored);
+  //   part B: O^T += V(t)^T P(t)^T on the MFMAs next to the row maxima of
+  //     tile t+1, which set the exponent reference of the next step;
+  //   the (rare) rescale of O, after the PV MFMAs; one barrier.
+  // O selects the buffers.
+  auto step = [&](auto O_, int t, f32x16 (&cur)[QB][KB], f32x16 (&nxt)[QB][KB]) {
+    constexpr int O = decltype(O_)::value;
+    char *const k_this = O ? k_lds1 : k_lds0;  // receives K(t+2)
+    char *const k_next = O ? k_lds0 : k_lds1;  // holds K(t+1)
+    char *const v_this = O ? v_lds1 : v_lds0;  // holds V(t)
+    char *const v_next = O ? v_lds0 : v_lds1;  // receives V(t+1)
+    if (t + 2 < t_end) copy_k(t + 2, k_this);
+    if (t + 1 < t_end) copy_v(t + 1, v_next);
+    score_first(nxt, k_next, t + 1);
+
+    // Part A.
     float psum[QB];
     bf16x8 pf[QB][KS];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-      psum[qb] = 0.0f;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         bf16x8 p;
+        float pv[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const float pv = fast_exp2(fmaf(sc[qb][ks >> 1][8 * (ks & 1) + j], c, -ms[qb]));
-          psum[qb] += pv;
-          p[j] = (bf16)pv;
+          pv[j] = fast_exp2(fmaf(cur[qb][ks >> 1][8 * (ks & 1) + j], c, -ms[qb]));
+          p[j] = (bf16)pv[j];
         }
+        // pairwise: a short dependency chain instead of 32 serial adds
+        const float s8 = ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
+        psum[qb] = ks == 0 ? s8 : psum[qb] + s8;
         pf[qb][ks] = p;
       }
     }
-    score_tile<D, BN, QB>(nxt, k_next, k_rd, qf);
-
+    score_tile<D, BN, QB, 1, DT, false>(nxt, k_next, k_rd, qf);
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) l[qb] = l[qb] * alpha[qb] + psum[qb];
+    for (int qb = 0; qb < QB; ++qb) l[qb] += psum[qb];
+
+    // Part B.
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
@@ -377,18 +390,53 @@ __global__ __launch_bounds__(RB *NPB * 64, ((QB == 1 && D <= 128) || D <= 64) ? 
         for (int qb = 0; qb < QB; ++qb)
           oacc[qb][d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[qb][ks], oacc[qb][d], 0, 0, 0);
       }
+    const bool has_next = t + 1 < t_end;
+    float mx[QB], alpha[QB];
+    bool raise[QB];
+    row_max(nxt, mx);
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      raise[qb] = (mx[qb] > m[qb] + kRescaleSlack) & has_next;  // no short-circuit branch
+      const float mnew = raise[qb] ? mx[qb] : m[qb];
+      const float msn = mnew == NEG_INF ? 0.0f : mnew;
+      alpha[qb] = fast_exp2(m[qb] - msn);
+      l[qb] *= alpha[qb];
+      m[qb] = mnew;
+      ms[qb] = msn;
+      // Keeps the row sum here, among the MFMAs: otherwise it is sunk past the
+      // rescale branch and holds the tile's probabilities live until then.
+      asm volatile("" : "+v"(l[qb]));
+    }
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+      if (__ballot(raise[qb])) {
+#pragma unroll
+        for (int d = 0; d < DB; ++d)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) oacc[qb][d][i] *= alpha[qb];
+      }
     wait_copies();
     __syncthreads();
   };
 
-  // Prologue: K(t0), V(t0), K(t0+1) copied; S(t0) computed.
+  // Prologue: K(t0), V(t0), K(t0+1) copied; S(t0) and its row maxima.
   f32x16 sa[QB][KB], sb[QB][KB];
   copy_k(t_begin, k_lds0);
   copy_v(t_begin, v_lds0);
   if (t_begin + 1 < t_end) copy_k(t_begin + 1, k_lds1);
   wait_copies();
   __syncthreads();
-  score_tile<D, BN, QB>(sa, k_lds0, k_rd, qf);
+  score_first(sa, k_lds0, t_begin);
+  score_tile<D, BN, QB, 1, DT, false>(sa, k_lds0, k_rd, qf);
+  {
+    float mx[QB];
+    row_max(sa, mx);
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      m[qb] = mx[qb];
+      ms[qb] = mx[qb] == NEG_INF ? 0.0f : mx[qb];
+    }
+  }
   __syncthreads();  // every wave is done with K(t0) before K(t0+2) lands in its buffer
 
   for (int t = t_begin; t < t_end; t += 2) {
