@@ -63,6 +63,32 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def derived_peaks() -> dict:
+    """Peaks re-derived from the device's own attributes (HIP runtime): dense
+    bf16 MFMA = CUs x 4 SIMDs x 1024 flop/clk (one 32x32x16 MFMA per 32
+    clocks) x peak engine clock; HBM = memory clock x bus width x 2 (DDR).
+    Reported next to the spec peaks the roofline uses."""
+    import ctypes
+
+    try:
+        hip = ctypes.CDLL("libamdhip64.so")
+    except OSError:
+        return {}
+
+    def attr(code: int) -> int:
+        v = ctypes.c_int(0)
+        return v.value if hip.hipDeviceGetAttribute(ctypes.byref(v), code, 0) == 0 else 0
+
+    # hipDeviceAttribute_t values of the ROCm 7 headers
+    clock_khz, mem_khz, bus_bits, cus = attr(5), attr(60), attr(59), attr(63)
+    out = {"sclk_max_MHz": clock_khz / 1e3, "mclk_MHz": mem_khz / 1e3, "mem_bus_bits": bus_bits}
+    if cus and clock_khz:
+        out["derived_bf16_dense_TFLOPs"] = round(cus * 4 * 1024 * clock_khz * 1e3 / 1e12, 1)
+    if mem_khz and bus_bits:
+        out["derived_hbm_GBps"] = round(mem_khz * 1e3 * 2 * bus_bits / 8 / 1e9, 1)
+    return out
+
+
 def gpu_bench(args) -> dict:
     import torch
 
@@ -78,6 +104,7 @@ def gpu_bench(args) -> dict:
     props = torch.cuda.get_device_properties(0)
     res["device"] = {"name": props.name, "cus": props.multi_processor_count,
                      "gcn_arch": getattr(props, "gcnArchName", "")}
+    res["device"].update(derived_peaks())
 
     with torch.cuda.stream(stream):
         # ---- achievable-bandwidth probe (read-only reduction over 4 GiB) ----

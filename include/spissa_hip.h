@@ -1,7 +1,7 @@
 /*
  * spissa_hip.h -- C ABI of the MI355X (gfx950) attention path for the Spissa
  * runtime: RoPE, the per-layer KV cache, cached SDPA (decode and causal GQA
- * prefill), and the Gemma 3 QK-norm.
+ * prefill), the Gemma 3 QK-norm, and the linear projections either side.
  *
  * Every symbol here replaces one Rust item of crates/spissa-runtime; the
  * citation next to each declaration names it (paths relative to the
@@ -223,6 +223,46 @@ int spissa_scaled_dot_product_attention(const float *q, size_t q_len, const floa
                                         size_t k_len, const float *v, size_t v_len,
                                         size_t seq_len, size_t num_heads, size_t head_dim,
                                         int causal, float *out, size_t out_len);
+
+/* ------------------------------------------------------------------------ */
+/* Linear projections: the q/k/v/o projections either side of the path.     */
+/* crates/spissa-runtime/src/streaming/linear.rs:269-576                    */
+/* (streaming_tile_linear_from_model) streams the weight from the model     */
+/* container chunk by chunk; here it is uploaded once and stays in HBM, and  */
+/* the call computes out[batch, out] = input[batch, in] x W[out, in]^T + bias */
+/* (ops.rs:62-105) in f32.                                                   */
+/* ------------------------------------------------------------------------ */
+
+/* Weight element types with a device kernel (spissa_container::DType Fp32,
+ * Fp16, Bf16). */
+typedef enum { SPISSA_DTYPE_F32 = 0, SPISSA_DTYPE_F16 = 1, SPISSA_DTYPE_BF16 = 2 } spissa_dtype;
+typedef struct spissa_linear_weight spissa_linear_weight;
+/* Uploads a row-major [out_features, in_features] weight whose little-endian
+ * element bytes are `data` (what a raw chunk of the container holds).
+ * data_bytes must equal out_features * in_features * element size
+ * (streaming/validation.rs:258-289: InvalidTensorData otherwise). */
+int spissa_linear_weight_new(spissa_session *s, int dtype, size_t out_features, size_t in_features,
+                             const void *data, size_t data_bytes, spissa_linear_weight **out);
+/* Frees the weight after the work queued on its session; call it before the
+ * session is destroyed. */
+void spissa_linear_weight_free(spissa_linear_weight *w);
+/* streaming/mod.rs:511-516 StreamingLinearConfig */
+typedef struct {
+    size_t batch;
+    size_t in_features;
+    size_t out_features;
+} spissa_linear_config;
+/* streaming/linear.rs:269-576 streaming_tile_linear_from_model, host buffers:
+ * validate_linear_shapes (input = batch * in_features, bias = out_features:
+ * Shape), then the weight shape against the config (Shape); bias may be
+ * NULL (Option::None). out receives batch * out_features floats. */
+int spissa_linear(const spissa_linear_weight *w, const float *input, size_t input_len,
+                  const float *bias, size_t bias_len, const spissa_linear_config *cfg,
+                  float *out, size_t out_len);
+/* Same on device buffers (d_input [batch, in], d_bias [out] or NULL,
+ * d_out [batch, out]), asynchronous on the session stream. */
+int spissa_linear_device(spissa_session *s, const spissa_linear_weight *w, const float *d_input,
+                         const float *d_bias, size_t batch, float *d_out);
 
 /* Prefill arithmetic for query_len > 1: SPISSA_PREFILL_BF16 (default) runs
  * the MFMA kernel; SPISSA_PREFILL_F32 runs the f32 SIMT kernel. */

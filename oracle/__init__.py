@@ -1,7 +1,8 @@
 """CPU oracle of the Spissa attention path -- TEST INFRASTRUCTURE ONLY.
 
 A ctypes wrapper over oracle/_build/libspissa_oracle.so, the C restatement of
-crates/spissa-runtime/src/rotary.rs:6-599 and ops.rs:159-291 (see
+crates/spissa-runtime/src/rotary.rs:6-599, ops.rs:62-105 and 159-291, and the
+weight decoding of tensor.rs and streaming/mod.rs (see
 spissa_oracle.c for per-function citations). Only tests/, __graft_entry__.smoke()
 and bench.py's cpu_baseline leg may import this package, and only as the
 checker or the timed CPU baseline. spissa_amd never imports it.
@@ -84,6 +85,10 @@ def load() -> C.CDLL:
         "or_is_global_layer": (C.c_int, [_sz, _sz]),
         "or_gemma_qk_prologue": (C.c_int, [_fp, _sz, _fp, _sz, _sz, _sz, _sz, _sz, _fp, _fp, C.c_float,
                                            C.c_float, C.c_float, _sz, C.c_float]),
+        "or_bf16_to_f32": (C.c_float, [C.c_uint16]),
+        "or_fp16_to_f32": (C.c_float, [C.c_uint16]),
+        "or_f32_to_bf16_rne": (C.c_uint16, [C.c_float]),
+        "or_linear": (C.c_int, [_fp, _sz, C.c_void_p, C.c_int, _sz, _fp, _sz, _sz, _sz, _sz, _fp]),
         "or_sdpa_many_threads": (C.c_int, [_sz, C.POINTER(_fp), C.POINTER(_fp), C.POINTER(_fp),
                                            C.POINTER(C.POINTER(KvC)), C.POINTER(AttnCfg),
                                            C.POINTER(_fp), C.c_int]),
@@ -229,3 +234,30 @@ def llama_cos_sin(pos, pair, rotary_dim, base, freq_scale=1.0):
     c, s = C.c_float(), C.c_float()
     load().or_llama_cos_sin(pos, pair, rotary_dim, base, freq_scale, C.byref(c), C.byref(s))
     return c.value, s.value
+
+
+DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
+
+
+def bf16_to_f32(bits: int) -> float:
+    return load().or_bf16_to_f32(bits)
+
+
+def fp16_to_f32(bits: int) -> float:
+    return load().or_fp16_to_f32(bits)
+
+
+def f32_to_bf16_rne(x: float) -> int:
+    return load().or_f32_to_bf16_rne(x)
+
+
+def linear(x, w, dtype, bias, batch, in_features, out_features) -> np.ndarray:
+    """ops.rs:62-105 over the decoded weight. w: float32 array (DTYPE_F32) or
+    uint16 array of bf16 / binary16 bits, [out, in] row-major."""
+    want = np.float32 if dtype == DTYPE_F32 else np.uint16
+    assert w.dtype == want and w.flags.c_contiguous
+    out = np.empty(batch * out_features, dtype=np.float32)
+    _check(load().or_linear(_p(x), x.size, w.ctypes.data_as(C.c_void_p), dtype, w.size, _p(bias),
+                            0 if bias is None else bias.size, batch, in_features, out_features, _p(out)))
+    return out
+

@@ -559,3 +559,72 @@ int or_sdpa_many_threads(size_t units, const float *const *q, const float *const
     }
     return st;
 }
+
+/* ---------------------------------------------------------------- linear */
+
+float or_bf16_to_f32(uint16_t bits) {
+    const uint32_t u = (uint32_t)bits << 16;
+    float f;
+    memcpy(&f, &u, sizeof f);
+    return f;
+}
+
+float or_fp16_to_f32(uint16_t bits) {
+    const uint32_t sign = (uint32_t)(bits & 0x8000u) << 16;
+    const unsigned exp = (bits >> 10) & 0x1fu, frac = bits & 0x3ffu;
+    uint32_t u;
+    if (exp == 0x1f) {
+        u = sign | 0x7f800000u | ((uint32_t)frac << 13); /* inf, nan */
+    } else if (exp != 0) {
+        u = sign | ((exp + 112u) << 23) | ((uint32_t)frac << 13); /* normal: rebias 15 -> 127 */
+    } else {
+        /* zero or subnormal: frac * 2^-24, exact in f32 */
+        float v = ldexpf((float)frac, -24);
+        memcpy(&u, &v, sizeof u);
+        u |= sign;
+    }
+    float f;
+    memcpy(&f, &u, sizeof f);
+    return f;
+}
+
+uint16_t or_f32_to_bf16_rne(float x) {
+    uint32_t b;
+    memcpy(&b, &x, sizeof b);
+    if ((b & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((b >> 16) | 0x0040u); /* NaN stays NaN */
+    return (uint16_t)((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
+}
+
+static float weight_at(const void *w, int dtype, size_t i) {
+    switch (dtype) {
+        case OR_DTYPE_BF16: return or_bf16_to_f32(((const uint16_t *)w)[i]);
+        case OR_DTYPE_F16: return or_fp16_to_f32(((const uint16_t *)w)[i]);
+        default: return ((const float *)w)[i];
+    }
+}
+
+int or_linear(const float *input, size_t input_len, const void *weight, int dtype, size_t weight_elems,
+              const float *bias, size_t bias_len, size_t batch, size_t in_features,
+              size_t out_features, float *out) {
+    if (input_len != batch * in_features)
+        return fail(OR_SHAPE, "input len %zu does not match batch*in_features = %zu", input_len,
+                    batch * in_features);
+    if (weight_elems != out_features * in_features)
+        return fail(OR_SHAPE, "weight len %zu does not match out_features*in_features = %zu", weight_elems,
+                    out_features * in_features);
+    if (bias && bias_len != out_features)
+        return fail(OR_SHAPE, "bias len %zu does not match out_features %zu", bias_len, out_features);
+    if (dtype != OR_DTYPE_F32 && dtype != OR_DTYPE_F16 && dtype != OR_DTYPE_BF16)
+        return fail(OR_INVALID, "unsupported weight dtype %d", dtype);
+    for (size_t b = 0; b < batch; ++b) {
+        const float *x = input + b * in_features;
+        for (size_t o = 0; o < out_features; ++o) {
+            float sum = bias ? bias[o] : 0.0f;
+            const size_t row = o * in_features;
+            for (size_t i = 0; i < in_features; ++i) sum += x[i] * weight_at(weight, dtype, row + i);
+            out[b * out_features + o] = sum;
+        }
+    }
+    return OR_OK;
+}
+

@@ -100,6 +100,23 @@ int or_scaled_dot_product_attention(const float *q, const float *k, const float 
                                     int causal, float *out);
 
 int or_is_global_layer(size_t layer_idx, size_t sliding_window_pattern);
+
+/* Weight element types (spissa_container::DType Fp32, Fp16, Bf16). */
+enum { OR_DTYPE_F32 = 0, OR_DTYPE_F16 = 1, OR_DTYPE_BF16 = 2 };
+/* tensor.rs:217-221 bf16_to_f32 */
+float or_bf16_to_f32(uint16_t bits);
+/* tensor.rs:166-215 fp16_to_f32 (exact binary16 decode) */
+float or_fp16_to_f32(uint16_t bits);
+/* streaming/mod.rs:366-374 f32_to_bf16_rne */
+uint16_t or_f32_to_bf16_rne(float x);
+/* ops.rs:62-105 linear over the weight decoded to f32 (tensor.rs:84-100
+ * decode_to_f32): out[b][o] = bias[o] + sum_i input[b][i] * w[o][i], the sum
+ * running from the bias in index order with each product rounded first. This
+ * is also the order of the reference's exact batch-1 row-block loop
+ * (streaming/kernels_raw16.rs:640-672). weight_elems counts elements. */
+int or_linear(const float *input, size_t input_len, const void *weight, int dtype, size_t weight_elems,
+              const float *bias, size_t bias_len, size_t batch, size_t in_features,
+              size_t out_features, float *out);
 int or_gemma_qk_prologue(float *q, size_t q_len, float *k, size_t k_len, size_t seq_len,
                          size_t q_heads, size_t kv_heads, size_t head_dim, const float *q_norm,
                          const float *k_norm, float eps, float rope_base,

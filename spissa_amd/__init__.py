@@ -1,11 +1,14 @@
 """spissa_amd -- MI355X (gfx950) attention path of the Spissa runtime.
 
-The package mirrors crates/spissa-runtime/src/rotary.rs and the ops the path
-uses, over the C ABI in include/spissa_hip.h (libspissa_hip.so). There is no
+The package mirrors crates/spissa-runtime/src/rotary.rs, the ops the path
+uses and the streaming linear projections either side of it, over the C ABI
+in include/spissa_hip.h (libspissa_hip.so). There is no
 CPU fallback: every call runs the HIP kernels.
 """
 from .errors import (ArgumentError, DeviceError, InvalidTensorDataError, ShapeError,  # noqa: F401
                      SpissaError)
+from .linear import (LinearModel, LinearWeight, StreamingLinearConfig,  # noqa: F401
+                     StreamingTileLinearConfig, linear, streaming_tile_linear_from_model)
 from .ops import is_global_layer, rms_norm, scaled_dot_product_attention  # noqa: F401
 from .rotary import (KvAttentionConfig, KvCache, RotaryEmbeddingConfig,  # noqa: F401
                      apply_gemma_rotary_inplace, apply_gpt_neox_rotary_inplace,

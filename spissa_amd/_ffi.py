@@ -24,9 +24,19 @@ ROPE_NEOX = 2
 PREFILL_BF16 = 0
 PREFILL_F32 = 1
 
+DTYPE_F32 = 0
+DTYPE_F16 = 1
+DTYPE_BF16 = 2
+
 c_size = C.c_size_t
 c_float_p = C.POINTER(C.c_float)
 c_void_p = C.c_void_p
+
+
+class LinearConfigC(C.Structure):
+    """spissa_linear_config (streaming/mod.rs:511-516)."""
+
+    _fields_ = [("batch", c_size), ("in_features", c_size), ("out_features", c_size)]
 
 
 class RotaryConfigC(C.Structure):
@@ -129,6 +139,13 @@ SIGNATURES = {
         C.c_int,
         [c_float_p, c_size, c_float_p, c_size, c_float_p, c_size, c_size, c_size, c_size, C.c_int,
          c_float_p, c_size]),
+    "spissa_linear_weight_new": (
+        C.c_int, [c_void_p, C.c_int, c_size, c_size, c_void_p, c_size, C.POINTER(c_void_p)]),
+    "spissa_linear_weight_free": (None, [c_void_p]),
+    "spissa_linear": (
+        C.c_int, [c_void_p, c_float_p, c_size, c_float_p, c_size, C.POINTER(LinearConfigC), c_float_p,
+                  c_size]),
+    "spissa_linear_device": (C.c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size, c_void_p]),
 }
 
 _lib = None

@@ -1144,3 +1144,130 @@ extern "C" int spissa_scaled_dot_product_attention(const float *q, size_t q_len,
   return spissa_scaled_dot_product_attention_with_cache(q, q_len, k, k_len, v, v_len, nullptr, &c, out, out_len);
   GUARD_END
 }
+
+// ------------------------------------------------------------------------
+// Linear projections (streaming/linear.rs:269-576)
+// ------------------------------------------------------------------------
+struct spissa_linear_weight {
+  spissa_session *session = nullptr;
+  int dtype = SPISSA_DTYPE_BF16;
+  size_t out_features = 0, in_features = 0;
+  void *data = nullptr;  // [out, in] row-major in HBM
+};
+
+static size_t dtype_size(int dtype) {
+  switch (dtype) {
+    case SPISSA_DTYPE_F32: return 4;
+    case SPISSA_DTYPE_F16: return 2;
+    case SPISSA_DTYPE_BF16: return 2;
+    default: return 0;
+  }
+}
+
+extern "C" int spissa_linear_weight_new(spissa_session *s, int dtype, size_t out_features, size_t in_features,
+                                        const void *data, size_t data_bytes, spissa_linear_weight **out) {
+  GUARD_BEGIN
+  if (!s || !out) return set_err(SPISSA_ERR_ARGUMENT, "null argument");
+  *out = nullptr;
+  const size_t es = dtype_size(dtype);
+  if (es == 0) return set_err(SPISSA_ERR_INVALID_TENSOR_DATA, "weight dtype %d has no device kernel", dtype);
+  size_t elems;
+  if (mul_ovf(out_features, in_features, &elems) || elems > (size_t)INT32_MAX * 8)
+    return set_err(SPISSA_ERR_SHAPE, "weight element count overflow");
+  if (out_features == 0 || in_features == 0 || out_features > INT32_MAX || in_features > INT32_MAX)
+    return set_err(SPISSA_ERR_SHAPE, "weight shape [%zu, %zu] is empty or too large", out_features, in_features);
+  // streaming/validation.rs:280-287: stored bytes must match shape x dtype
+  if (data_bytes != elems * es)
+    return set_err(SPISSA_ERR_INVALID_TENSOR_DATA, "weight holds %zu bytes, shape [%zu, %zu] needs %zu", data_bytes,
+                   out_features, in_features, elems * es);
+  if (!data) return set_err(SPISSA_ERR_ARGUMENT, "data is null");
+  std::unique_ptr<spissa_linear_weight> w(new spissa_linear_weight);
+  w->session = s;
+  w->dtype = dtype;
+  w->out_features = out_features;
+  w->in_features = in_features;
+  HIP_TRY(hipSetDevice(s->device));
+  HIP_TRY(hipMalloc(&w->data, data_bytes));
+  hipError_t e = hipMemcpyAsync(w->data, data, data_bytes, hipMemcpyHostToDevice, s->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+  if (e != hipSuccess) {
+    (void)hipFree(w->data);
+    return set_err(SPISSA_ERR_DEVICE, "weight upload failed: %s", hipGetErrorString(e));
+  }
+  *out = w.release();
+  return SPISSA_OK;
+  GUARD_END
+}
+
+extern "C" void spissa_linear_weight_free(spissa_linear_weight *w) {
+  if (!w) return;
+  (void)hipSetDevice(w->session->device);
+  (void)hipStreamSynchronize(w->session->stream);
+  if (w->data) (void)hipFree(w->data);
+  delete w;
+}
+
+static int linear_launch(spissa_session *s, const spissa_linear_weight *w, const float *d_x, const float *d_bias,
+                         size_t batch, float *d_out) {
+  if (batch == 0) return SPISSA_OK;
+  if (batch > INT32_MAX) return set_err(SPISSA_ERR_SHAPE, "batch %zu too large", batch);
+  LinearArgs a{};
+  a.w = w->data;
+  a.x = d_x;
+  a.bias = d_bias;
+  a.out = d_out;
+  a.M = (int)batch;
+  a.N = (int)w->out_features;
+  a.K = (int)w->in_features;
+  a.dtype = w->dtype;
+  int path = linear_path(a.dtype, a.M, a.K);
+  // the vector kernels read 16-byte pieces of x and of the weight rows
+  if (path != kLinearGeneric && (reinterpret_cast<uintptr_t>(d_x) & 15)) path = kLinearGeneric;
+  HIP_TRY(hipSetDevice(s->device));
+  HIP_TRY(launch_linear(s->stream, a, path));
+  return SPISSA_OK;
+}
+
+extern "C" int spissa_linear(const spissa_linear_weight *w, const float *input, size_t input_len, const float *bias,
+                             size_t bias_len, const spissa_linear_config *cfg, float *out, size_t out_len) {
+  GUARD_BEGIN
+  if (!w || !cfg) return set_err(SPISSA_ERR_ARGUMENT, "null argument");
+  // streaming/validation.rs:225-247 validate_linear_shapes
+  size_t want_in, want_out;
+  if (mul_ovf(cfg->batch, cfg->in_features, &want_in) || mul_ovf(cfg->batch, cfg->out_features, &want_out))
+    return set_err(SPISSA_ERR_SHAPE, "linear shape overflow");
+  if (input_len != want_in)
+    return set_err(SPISSA_ERR_SHAPE, "input len %zu does not match batch*in_features = %zu", input_len, want_in);
+  if (bias && bias_len != cfg->out_features)
+    return set_err(SPISSA_ERR_SHAPE, "bias len %zu does not match out_features %zu", bias_len, cfg->out_features);
+  // streaming/validation.rs:258-279 validate_weight_tensor (shape)
+  if (w->out_features != cfg->out_features || w->in_features != cfg->in_features)
+    return set_err(SPISSA_ERR_SHAPE, "weight shape [%zu, %zu] does not match requested [%zu, %zu]", w->out_features,
+                   w->in_features, cfg->out_features, cfg->in_features);
+  if (out_len != want_out)
+    return set_err(SPISSA_ERR_SHAPE, "output holds %zu floats, need %zu", out_len, want_out);
+  if (want_out == 0) return SPISSA_OK;
+  if ((want_in && !input) || !out) return set_err(SPISSA_ERR_ARGUMENT, "null buffer");
+  spissa_session *s = w->session;
+  float *r[3];
+  ST_TRY(io_regions(s, {want_in, bias ? cfg->out_features : 0, want_out}, r));
+  HIP_TRY(hipSetDevice(s->device));
+  ST_TRY(h2d(s, r[0], input, want_in * sizeof(float)));
+  if (bias) ST_TRY(h2d(s, r[1], bias, cfg->out_features * sizeof(float)));
+  ST_TRY(linear_launch(s, w, r[0], bias ? r[1] : nullptr, cfg->batch, r[2]));
+  ST_TRY(d2h(s, out, r[2], want_out * sizeof(float)));
+  return sync_stream(s);
+  GUARD_END
+}
+
+extern "C" int spissa_linear_device(spissa_session *s, const spissa_linear_weight *w, const float *d_input,
+                                    const float *d_bias, size_t batch, float *d_out) {
+  GUARD_BEGIN
+  if (!s || !w) return set_err(SPISSA_ERR_ARGUMENT, "null argument");
+  if (w->session->device != s->device)
+    return set_err(SPISSA_ERR_ARGUMENT, "weight lives on device %d, session on %d", w->session->device, s->device);
+  if (batch && (!d_input || !d_out)) return set_err(SPISSA_ERR_ARGUMENT, "null buffer");
+  return linear_launch(s, w, d_input, d_bias, batch, d_out);
+  GUARD_END
+}
+

@@ -68,6 +68,17 @@ struct DecodeArgs {
   SeqDesc seq[kMaxDecodeBatch];
 };
 
+// Linear projection out[M, N] = x[M, K] x W[N, K]^T + bias (linear.hip).
+struct LinearArgs {
+  const void *w;       // [N, K] row-major, dtype
+  const float *x;      // [M, K]
+  const float *bias;   // [N] or null
+  float *out;          // [M, N]
+  int M, N, K;
+  int dtype;           // spissa_dtype
+};
+enum { kLinearGemv = 0, kLinearGemm = 1, kLinearGeneric = 2 };
+
 struct PrefillArgs {
   const float *q;     // [S, Hq, D] f32
   float *out;         // [S, Hq, D] f32
@@ -131,6 +142,11 @@ hipError_t launch_prefill(hipStream_t st, const PrefillArgs &a, int D);
 // Merges the key splits of a split prefill into `out` (and the error flag).
 hipError_t launch_prefill_combine(hipStream_t st, const PrefillArgs &a, int D);
 hipError_t launch_generic(hipStream_t st, const GenericArgs &a);
+// Kernel choice for a linear projection (kLinearGemv for M <= 4, kLinearGemm
+// for bf16 weights with M > 4 and K % 32 == 0, else kLinearGeneric), and its
+// launch. The vector paths also need 16-byte aligned x and weight rows.
+int linear_path(int dtype, long M, long K);
+hipError_t launch_linear(hipStream_t st, const LinearArgs &a, int path);
 
 // Keys per split of a decode launch: total_rows = key rows summed over all
 // (sequence, KV head, head block) triples; max_keys = longest visible range.

@@ -1,0 +1,399 @@
+// linear.hip -- the projections on either side of the attention path:
+// out[M, N] = x[M, K] x W[N, K]^T + bias[N] with f32 activations and output
+// and the weight resident in HBM as bf16, f16 or f32
+// (crates/spissa-runtime/src/streaming/linear.rs:269-576,
+// streaming_tile_linear_from_model, whose exact default accumulates each
+// output as bias + a sequential f32 dot: streaming/kernels_raw16.rs:532-600,
+// streaming/mod.rs:311-320; the plain form is ops.rs:62-105 linear).
+//
+// Three kernels:
+//  - linear_gemv_kernel (M <= 4 tokens, the decode projections): bound by the
+//    weight bytes. A wave owns two weight rows; each lane streams 16-byte
+//    pieces of them (8 bf16/f16 or 4 f32 weights) with the matching
+//    activations from the cache, accumulates in f32, and the wave sums its
+//    lanes with DPP and permlane exchanges.
+//  - linear_gemm_kernel (bf16 weights, M > 4, K % 32 == 0: prefill): MFMA
+//    v_mfma_f32_32x32x16_bf16 on 128 x 128 output tiles, 32-deep k tiles in
+//    LDS (weights copied global -> LDS with global_load_lds_dwordx4,
+//    activations converted in registers). Each f32 activation is split into
+//    bf16 hi = rne(x) and lo = rne(x - hi), and both halves meet the bf16
+//    weight: the products are exact in f32 and the residual of the split is
+//    below 2^-16 |x|, so the result carries f32-level error rather than bf16.
+//  - linear_generic_kernel (everything else): one thread per output, the
+//    reference's sequential f32 sum from the bias with separately rounded
+//    products, so its results equal the reference's linear bit for bit.
+#include "internal.hpp"
+
+namespace spissa {
+
+namespace {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((address_space(3))) void lds_void;
+
+// 16 bytes of weights -> f32 (exact for every dtype).
+template <typename WT>
+struct WChunk;
+template <>
+struct WChunk<float> {
+  static constexpr int N = 4;
+  __device__ static void get(const uint4 r, float (&f)[4]) {
+    f[0] = __uint_as_float(r.x);
+    f[1] = __uint_as_float(r.y);
+    f[2] = __uint_as_float(r.z);
+    f[3] = __uint_as_float(r.w);
+  }
+};
+template <>
+struct WChunk<__bf16> {
+  static constexpr int N = 8;
+  __device__ static void get(const uint4 r, float (&f)[8]) {
+    const unsigned u[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = __uint_as_float(u[i] << 16);
+      f[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+    }
+  }
+};
+template <>
+struct WChunk<_Float16> {
+  static constexpr int N = 8;
+  __device__ static void get(const uint4 r, float (&f)[8]) {
+    const unsigned u[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = (float)__builtin_bit_cast(_Float16, (unsigned short)(u[i] & 0xffffu));
+      f[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (unsigned short)(u[i] >> 16));
+    }
+  }
+};
+
+template <int CTRL>
+__device__ __forceinline__ float dpp0(float v) {
+  return __builtin_amdgcn_update_dpp(0.0f, v, CTRL, 0xf, 0xf, false);
+}
+
+// Sum over the 64 lanes of a wave (every lane receives it).
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp0<0xB1>(v);   // lane ^ 1
+  v += dpp0<0x4E>(v);   // lane ^ 2
+  v += dpp0<0x141>(v);  // row_half_mirror
+  v += dpp0<0x140>(v);  // row_mirror
+  auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+  auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+}
+
+constexpr int kGemvRowsPerWave = 2;
+
+}  // namespace
+
+// Grid: ceil(N / (4 * kGemvRowsPerWave)) workgroups of 256 threads. K is a
+// multiple of the chunk width (8 for 16-bit weights, 4 for f32).
+template <typename WT, int NB>
+__global__ __launch_bounds__(256) void linear_gemv_kernel(const LinearArgs a) {
+  using C = WChunk<WT>;
+  constexpr int EPC = C::N, RW = kGemvRowsPerWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int r0 = (blockIdx.x * 4 + wave) * RW;
+  if (r0 >= a.N) return;  // uniform per wave
+  const int nch = a.K / EPC;
+  const char *wb = reinterpret_cast<const char *>(a.w);
+  long roff[RW];
+#pragma unroll
+  for (int i = 0; i < RW; ++i) roff[i] = (long)min(r0 + i, a.N - 1) * a.K * (long)sizeof(WT);
+
+  float acc[RW][NB];
+#pragma unroll
+  for (int i = 0; i < RW; ++i)
+#pragma unroll
+    for (int t = 0; t < NB; ++t) acc[i][t] = 0.0f;
+
+#pragma unroll 2
+  for (int c = lane; c < nch; c += 64) {
+    uint4 raw[RW];
+#pragma unroll
+    for (int i = 0; i < RW; ++i) raw[i] = *reinterpret_cast<const uint4 *>(wb + roff[i] + (long)c * 16);
+    float xv[NB][EPC];
+#pragma unroll
+    for (int t = 0; t < NB; ++t) {
+      const float *xp = a.x + (long)t * a.K + (long)c * EPC;
+#pragma unroll
+      for (int j = 0; j < EPC; j += 4) {
+        const float4 v = *reinterpret_cast<const float4 *>(xp + j);
+        xv[t][j] = v.x;
+        xv[t][j + 1] = v.y;
+        xv[t][j + 2] = v.z;
+        xv[t][j + 3] = v.w;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < RW; ++i) {
+      float wf[EPC];
+      C::get(raw[i], wf);
+#pragma unroll
+      for (int t = 0; t < NB; ++t)
+#pragma unroll
+        for (int j = 0; j < EPC; ++j) acc[i][t] = fmaf(wf[j], xv[t][j], acc[i][t]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < RW; ++i)
+#pragma unroll
+    for (int t = 0; t < NB; ++t) acc[i][t] = wave_sum(acc[i][t]);
+  if (lane < RW * NB) {
+    const int i = lane / NB, t = lane % NB;
+    const int r = r0 + i;
+    float v = 0.0f;
+#pragma unroll
+    for (int ii = 0; ii < RW; ++ii)
+#pragma unroll
+      for (int tt = 0; tt < NB; ++tt) v = (ii == i && tt == t) ? acc[ii][tt] : v;
+    if (r < a.N) a.out[(long)t * a.N + r] = (a.bias ? a.bias[r] : 0.0f) + v;
+  }
+}
+
+namespace {
+constexpr int kBM = 128, kBN = 128, kBK = 32;  // GEMM tiles
+constexpr int kRowBytes = kBK * 2;              // one bf16 tile row: 64 bytes, four 16-byte chunks
+
+// Chunk swizzle of a 64-byte LDS row: any 8 aligned consecutive rows reading
+// the same chunk hit 8 distinct 16-byte groups modulo 128 bytes.
+__device__ __forceinline__ int swz4(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
+
+__device__ __forceinline__ unsigned short bf16_rne_bits(float x) {
+  return __builtin_bit_cast(unsigned short, (__bf16)x);
+}
+}  // namespace
+
+// Grid: ceil(M / 128) * ceil(N / 128) workgroups of 256 threads (2 x 2 waves,
+// 64 x 64 outputs each). K % 32 == 0. Rows past M or N are read clamped and
+// not stored.
+__global__ __launch_bounds__(256, 2) void linear_gemm_kernel(const LinearArgs a) {
+  __shared__ __attribute__((aligned(1024))) char w_lds0[kBN * kRowBytes];
+  __shared__ __attribute__((aligned(1024))) char w_lds1[kBN * kRowBytes];
+  __shared__ __attribute__((aligned(1024))) char xh_lds0[kBM * kRowBytes];
+  __shared__ __attribute__((aligned(1024))) char xh_lds1[kBM * kRowBytes];
+  __shared__ __attribute__((aligned(1024))) char xl_lds0[kBM * kRowBytes];
+  __shared__ __attribute__((aligned(1024))) char xl_lds1[kBM * kRowBytes];
+
+  const int tiles_n = (a.N + kBN - 1) / kBN;
+  const int tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
+  const int m0 = tm * kBM, n0 = tn * kBN;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int wm = wave >> 1, wn = wave & 1;  // the wave's 64 x 64 quadrant
+  const int lr = lane & 31, hl = lane >> 5;
+  const int nk = a.K / kBK;
+
+  // Weight copies: 8 KB per tile = 8 copies of 1 KB, two per wave. Copy j of
+  // wave w fills LDS bytes [(2w + j) * 1024, +1024); lane l's 16 bytes land at
+  // +16 l, i.e. row R = byte / 64, position p, which holds chunk p ^ swz4(R).
+  const char *wg = reinterpret_cast<const char *>(a.w);
+  long w_src[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int byte = (2 * wave + j) * 1024 + lane * 16;
+    const int row = byte / kRowBytes, p = (byte % kRowBytes) / 16;
+    const int n = min(n0 + row, a.N - 1);
+    w_src[j] = (long)n * a.K * 2 + 16 * (p ^ swz4(row));
+  }
+  auto copy_w = [&](int kt, char *dst) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      __builtin_amdgcn_global_load_lds(wg + w_src[j] + (long)kt * kBK * 2, (lds_void *)(dst + (2 * wave + j) * 1024),
+                                       16, 0, 0);
+  };
+  // Activations: thread t loads row t / 2, columns 16 (t % 2) + [0, 16) of the
+  // k tile, splits them and writes 32 bytes of hi and of lo (chunks 2 (t % 2)
+  // and 2 (t % 2) + 1 of the row).
+  const int xr = tid >> 1, xc = tid & 1;
+  const float *xg = a.x + (long)min(m0 + xr, a.M - 1) * a.K + 16 * xc;
+  float4 xv[4];
+  auto load_x = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xv[i] = *reinterpret_cast<const float4 *>(xg + (long)kt * kBK + 4 * i);
+  };
+  auto store_x = [&](char *hi, char *lo) {
+    const float f[16] = {xv[0].x, xv[0].y, xv[0].z, xv[0].w, xv[1].x, xv[1].y, xv[1].z, xv[1].w,
+                         xv[2].x, xv[2].y, xv[2].z, xv[2].w, xv[3].x, xv[3].y, xv[3].z, xv[3].w};
+    unsigned h[8], l[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const unsigned short h0 = bf16_rne_bits(f[2 * i]), h1 = bf16_rne_bits(f[2 * i + 1]);
+      const float r0 = f[2 * i] - __uint_as_float((unsigned)h0 << 16);
+      const float r1 = f[2 * i + 1] - __uint_as_float((unsigned)h1 << 16);
+      h[i] = (unsigned)h0 | ((unsigned)h1 << 16);
+      l[i] = (unsigned)bf16_rne_bits(r0) | ((unsigned)bf16_rne_bits(r1) << 16);
+    }
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc) {
+      const int off = xr * kRowBytes + 16 * ((2 * xc + cc) ^ swz4(xr));
+      *reinterpret_cast<uint4 *>(hi + off) = make_uint4(h[4 * cc], h[4 * cc + 1], h[4 * cc + 2], h[4 * cc + 3]);
+      *reinterpret_cast<uint4 *>(lo + off) = make_uint4(l[4 * cc], l[4 * cc + 1], l[4 * cc + 2], l[4 * cc + 3]);
+    }
+  };
+
+  // Fragment offsets: block b of the quadrant, 16-deep k step s: row
+  // 32 b + lr, chunk 2 s + hl (32 b leaves swz4 unchanged).
+  unsigned a_rd[2][2], b_rd[2][2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int ra = wm * 64 + 32 * b + lr, rb = wn * 64 + 32 * b + lr;
+      a_rd[b][s] = ra * kRowBytes + 16 * ((2 * s + hl) ^ swz4(ra));
+      b_rd[b][s] = rb * kRowBytes + 16 * ((2 * s + hl) ^ swz4(rb));
+    }
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  auto compute = [&](const char *wl, const char *xh, const char *xl) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      bf16x8 fa_h[2], fa_l[2], fb[2];
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        fa_h[b] = *reinterpret_cast<const bf16x8 *>(xh + a_rd[b][s]);
+        fa_l[b] = *reinterpret_cast<const bf16x8 *>(xl + a_rd[b][s]);
+        fb[b] = *reinterpret_cast<const bf16x8 *>(wl + b_rd[b][s]);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa_h[i], fb[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa_l[i], fb[j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  // Prologue: tile 0 into buffer 0.
+  copy_w(0, w_lds0);
+  load_x(0);
+  store_x(xh_lds0, xl_lds0);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's weight copies
+  __syncthreads();
+
+  for (int kt = 0; kt < nk; kt += 2) {
+    // even step: compute buffer 0, fill buffer 1
+    if (kt + 1 < nk) {
+      copy_w(kt + 1, w_lds1);
+      load_x(kt + 1);
+    }
+    compute(w_lds0, xh_lds0, xl_lds0);
+    if (kt + 1 < nk) store_x(xh_lds1, xl_lds1);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+    if (kt + 1 >= nk) break;
+    // odd step: compute buffer 1, fill buffer 0
+    if (kt + 2 < nk) {
+      copy_w(kt + 2, w_lds0);
+      load_x(kt + 2);
+    }
+    compute(w_lds1, xh_lds1, xl_lds1);
+    if (kt + 2 < nk) store_x(xh_lds0, xl_lds0);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+  }
+
+  // Accumulator layout: element e of lane l is row 8 (e / 4) + 4 hl + e % 4,
+  // column lr of its 32 x 32 block.
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int n = n0 + wn * 64 + 32 * j + lr;
+    if (n >= a.N) continue;
+    const float bn = a.bias ? a.bias[n] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = m0 + wm * 64 + 32 * i + 8 * (e >> 2) + 4 * hl + (e & 3);
+        if (m < a.M) a.out[(long)m * a.N + n] = bn + acc[i][j][e];
+      }
+  }
+}
+
+// One thread per output: the sum starts at the bias and adds x[m][k] * w[n][k]
+// in index order, each product rounded first (ops.rs:94-103; also the exact
+// batch-1 row-block loop of streaming/kernels_raw16.rs:640-672).
+template <typename WT>
+__global__ __launch_bounds__(256) void linear_generic_kernel(const LinearArgs a) {
+#pragma clang fp contract(off)
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (long)a.M * a.N) return;
+  const int m = (int)(idx / a.N), n = (int)(idx % a.N);
+  const WT *w = reinterpret_cast<const WT *>(a.w) + (long)n * a.K;
+  const float *x = a.x + (long)m * a.K;
+  float sum = a.bias ? a.bias[n] : 0.0f;
+  for (int k = 0; k < a.K; ++k) {
+    float wf;
+    if constexpr (sizeof(WT) == 4) wf = (float)w[k];
+    else if constexpr (__is_same(WT, __bf16)) wf = __uint_as_float((unsigned)__builtin_bit_cast(unsigned short, w[k]) << 16);
+    else wf = (float)w[k];
+    const float p = x[k] * wf;
+    sum = sum + p;
+  }
+  a.out[idx] = sum;
+}
+
+namespace {
+template <typename WT>
+hipError_t launch_gemv(hipStream_t st, const LinearArgs &a) {
+  const unsigned grid = (unsigned)((a.N + 4 * kGemvRowsPerWave - 1) / (4 * kGemvRowsPerWave));
+  switch (a.M) {
+    case 1: hipLaunchKernelGGL((linear_gemv_kernel<WT, 1>), dim3(grid), dim3(256), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((linear_gemv_kernel<WT, 2>), dim3(grid), dim3(256), 0, st, a); break;
+    case 3: hipLaunchKernelGGL((linear_gemv_kernel<WT, 3>), dim3(grid), dim3(256), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((linear_gemv_kernel<WT, 4>), dim3(grid), dim3(256), 0, st, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+template <typename WT>
+hipError_t launch_generic_linear(hipStream_t st, const LinearArgs &a) {
+  const long n = (long)a.M * a.N;
+  hipLaunchKernelGGL((linear_generic_kernel<WT>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+template <typename WT>
+hipError_t launch_typed(hipStream_t st, const LinearArgs &a, int path) {
+  if (path == kLinearGemv) return launch_gemv<WT>(st, a);
+  return launch_generic_linear<WT>(st, a);
+}
+}  // namespace
+
+int linear_path(int dtype, long M, long K) {
+  const int epc = dtype == SPISSA_DTYPE_F32 ? 4 : 8;
+  if (dtype == SPISSA_DTYPE_BF16 && M > 4 && K % kBK == 0) return kLinearGemm;
+  if (M <= 4 && K % epc == 0) return kLinearGemv;
+  return kLinearGeneric;
+}
+
+hipError_t launch_linear(hipStream_t st, const LinearArgs &a, int path) {
+  if (a.M <= 0 || a.N <= 0) return hipSuccess;
+  if (path == kLinearGemm) {
+    if (a.dtype != SPISSA_DTYPE_BF16 || a.K % kBK != 0) return hipErrorInvalidValue;
+    const long grid = (long)((a.M + kBM - 1) / kBM) * ((a.N + kBN - 1) / kBN);
+    hipLaunchKernelGGL(linear_gemm_kernel, dim3((unsigned)grid), dim3(256), 0, st, a);
+    return hipGetLastError();
+  }
+  switch (a.dtype) {
+    case SPISSA_DTYPE_F32: return launch_typed<float>(st, a, path);
+    case SPISSA_DTYPE_BF16: return launch_typed<__bf16>(st, a, path);
+    case SPISSA_DTYPE_F16: return launch_typed<_Float16>(st, a, path);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace spissa

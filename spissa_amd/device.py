@@ -164,3 +164,14 @@ class Session:
 
     def append(self, cache: KvCache, k, v, token_count: int) -> None:
         cache.append_device(_dev(k, "k"), _dev(v, "v"), token_count)
+
+    def linear_weight(self, data, dtype: int, out_features: int, in_features: int):
+        """A weight resident on this session's device (see spissa_amd.linear.LinearWeight)."""
+        from .linear import LinearWeight
+
+        return LinearWeight(data, dtype, out_features, in_features, session=self)
+
+    def linear(self, weight, x, bias, batch: int, out) -> None:
+        """out[batch, out] = x[batch, in] x W^T + bias on device tensors (bias may be None)."""
+        check(self._lib.spissa_linear_device(self.handle, weight.handle, _dev(x, "x"),
+                                             _dev(bias, "bias") or None, batch, _dev(out, "out")))
