@@ -66,7 +66,8 @@ def log(msg: str) -> None:
 def derived_peaks() -> dict:
     """Peaks re-derived from the device's own attributes (HIP runtime): dense
     bf16 MFMA = CUs x 4 SIMDs x 1024 flop/clk (one 32x32x16 MFMA per 32
-    clocks) x peak engine clock; HBM = memory clock x bus width x 2 (DDR).
+    clocks) x peak engine clock; HBM = memory clock x bus width x 4 (HBM3E
+    moves 4 bits per pin per reported memory clock: 8 Gb/s at 2000 MHz).
     Reported next to the spec peaks the roofline uses."""
     import ctypes
 
@@ -85,7 +86,7 @@ def derived_peaks() -> dict:
     if cus and clock_khz:
         out["derived_bf16_dense_TFLOPs"] = round(cus * 4 * 1024 * clock_khz * 1e3 / 1e12, 1)
     if mem_khz and bus_bits:
-        out["derived_hbm_GBps"] = round(mem_khz * 1e3 * 2 * bus_bits / 8 / 1e9, 1)
+        out["derived_hbm_GBps"] = round(mem_khz * 1e3 * 4 * bus_bits / 8 / 1e9, 1)
     return out
 
 
@@ -272,8 +273,59 @@ def gpu_bench(args) -> dict:
                 "tokens_per_s": PREFILL_S * 1e3 / ms_p,
                 "flop_per_layer": fl,
             }
-            del g_p
+            del g_p, pq, pk, pv, po
+            torch.cuda.empty_cache()
+
+        # ---- the projections either side (q/k/v fused, bf16 weights) ----
+        if not args.decode_only:
+            log("timing projections")
+            res["projections"] = projection_bench(sess, stream, gen, dev, args, time_graph)
     return res
+
+
+def projection_bench(sess, stream, gen, dev, args, time_graph) -> dict:
+    """Llama-3.2-3B fused q/k/v projection (5120 x 3072 bf16 weight, one per
+    layer) at decode batch 1 and 16 and at the 4096-token prefill."""
+    import numpy as np
+    import torch
+
+    from spissa_amd.linear import DTYPE_BF16
+
+    hid, qkv = HQ * D, (HQ + 2 * HKV) * D
+    host = (np.random.default_rng(11).standard_normal(qkv * hid).astype(np.float32) * 0.02)
+    host = (host.view(np.uint32) >> 16).astype(np.uint16)  # bf16 bits (truncated: data only)
+    weights = [sess.linear_weight(host, DTYPE_BF16, qkv, hid) for _ in range(LAYERS)]
+    out = {}
+    for batch, layers in ((1, LAYERS), (16, LAYERS), (PREFILL_S, 4)):
+        with torch.cuda.stream(stream):
+            x = torch.randn(batch * hid, generator=gen, device=dev)
+            y = torch.empty(batch * qkv, device=dev)
+
+        def step():
+            for l in range(layers):
+                sess.linear(weights[l], x, None, batch, y)
+
+        step()
+        sess.sync()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            step()
+        ms = time_graph(g, max(3, args.steps // 2), 2)
+        us = ms * 1e3 / layers
+        wbytes = qkv * hid * 2
+        rec = {"us_per_layer": round(us, 3), "weight_GBps": round(wbytes / (us * 1e-6) / 1e9, 1),
+               "TFLOPs": round(2.0 * batch * qkv * hid / (us * 1e-6) / 1e12, 2)}
+        if batch == 1:
+            rec["hbm_frac"] = round(rec["weight_GBps"] / HBM_PEAK_GBS, 4)
+        if batch == PREFILL_S:
+            # the split activations double the MFMA work
+            rec["mfma_TFLOPs"] = round(2 * rec["TFLOPs"], 2)
+            rec["mfma_frac"] = round(2 * rec["TFLOPs"] / BF16_PEAK_TFLOPS, 4)
+        out[f"qkv_b{batch}"] = rec
+        del g, x, y
+    del weights
+    torch.cuda.empty_cache()
+    return out
 
 
 def cpu_baseline(args) -> dict:
@@ -398,6 +450,10 @@ def main() -> int:
         line["roofline_prefill"] = {"bound": "mfma", "achieved": round(p["TFLOPs"], 2), "peak": BF16_PEAK_TFLOPS,
                                     "unit": "TFLOP/s", "frac": round(p["TFLOPs"] / BF16_PEAK_TFLOPS, 4),
                                     "dtype": "bf16 MFMA, f32 accumulate"}
+    if "projections" in res:
+        line["projections"] = {"workload": "llama-3.2-3B fused q/k/v projection, 5120 x 3072 bf16 weight "
+                                           "resident in HBM, f32 activations and output",
+                               **res["projections"]}
     if cpu is not None:
         line["cpu_baseline"] = cpu
     print(json.dumps(line), flush=True)

@@ -77,7 +77,7 @@ struct LinearArgs {
   int M, N, K;
   int dtype;           // spissa_dtype
 };
-enum { kLinearGemv = 0, kLinearGemm = 1, kLinearGeneric = 2 };
+enum { kLinearGemv = 0, kLinearGemm = 1, kLinearGeneric = 2, kLinearSkinny = 3 };
 
 struct PrefillArgs {
   const float *q;     // [S, Hq, D] f32
@@ -142,9 +142,9 @@ hipError_t launch_prefill(hipStream_t st, const PrefillArgs &a, int D);
 // Merges the key splits of a split prefill into `out` (and the error flag).
 hipError_t launch_prefill_combine(hipStream_t st, const PrefillArgs &a, int D);
 hipError_t launch_generic(hipStream_t st, const GenericArgs &a);
-// Kernel choice for a linear projection (kLinearGemv for M <= 4, kLinearGemm
-// for bf16 weights with M > 4 and K % 32 == 0, else kLinearGeneric), and its
-// launch. The vector paths also need 16-byte aligned x and weight rows.
+// Kernel choice for a linear projection (kLinearGemv for M <= 4; for bf16
+// weights kLinearSkinny for M <= 64 with K % 128 == 0, kLinearGemm for larger M
+// with K % 32 == 0; else kLinearGeneric), and its launch. The vector paths also need 16-byte aligned x and weight rows.
 int linear_path(int dtype, long M, long K);
 hipError_t launch_linear(hipStream_t st, const LinearArgs &a, int path);
 

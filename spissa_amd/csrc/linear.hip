@@ -6,13 +6,16 @@
 // output as bias + a sequential f32 dot: streaming/kernels_raw16.rs:532-600,
 // streaming/mod.rs:311-320; the plain form is ops.rs:62-105 linear).
 //
-// Three kernels:
+// Four kernels:
 //  - linear_gemv_kernel (M <= 4 tokens, the decode projections): bound by the
 //    weight bytes. A wave owns two weight rows; each lane streams 16-byte
 //    pieces of them (8 bf16/f16 or 4 f32 weights) with the matching
 //    activations from the cache, accumulates in f32, and the wave sums its
 //    lanes with DPP and permlane exchanges.
-//  - linear_gemm_kernel (bf16 weights, M > 4, K % 32 == 0: prefill): MFMA
+//  - linear_skinny_kernel (bf16 weights, 5 <= M <= 64, K % 128 == 0: batched
+//    decode): weight fragments straight from HBM into 16x16x32 MFMAs, the
+//    activations split as below, K split over the workgroup's four waves.
+//  - linear_gemm_kernel (bf16 weights, M > 64, K % 32 == 0: prefill): MFMA
 //    v_mfma_f32_32x32x16_bf16 on 128 x 128 output tiles, 32-deep k tiles in
 //    LDS (weights copied global -> LDS with global_load_lds_dwordx4,
 //    activations converted in registers). Each f32 activation is split into
@@ -22,6 +25,8 @@
 //  - linear_generic_kernel (everything else): one thread per output, the
 //    reference's sequential f32 sum from the bias with separately rounded
 //    products, so its results equal the reference's linear bit for bit.
+#include <type_traits>
+
 #include "internal.hpp"
 
 namespace spissa {
@@ -164,17 +169,28 @@ constexpr int kRowBytes = kBK * 2;              // one bf16 tile row: 64 bytes, 
 // the same chunk hit 8 distinct 16-byte groups modulo 128 bytes.
 __device__ __forceinline__ int swz4(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
 
-__device__ __forceinline__ unsigned short bf16_rne_bits(float x) {
-  return __builtin_bit_cast(unsigned short, (__bf16)x);
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+
+// (rne(a), rne(b)) as bf16 bits, a in the low half.
+__device__ __forceinline__ unsigned bf16x2_rne(float a, float b) {
+  return __builtin_bit_cast(unsigned, __builtin_convertvector((f32x2){a, b}, bf16x2));
 }
 }  // namespace
 
 // Grid: ceil(M / 128) * ceil(N / 128) workgroups of 256 threads (2 x 2 waves,
 // 64 x 64 outputs each). K % 32 == 0. Rows past M or N are read clamped and
 // not stored.
+// Pipeline, per 32-deep k tile t: the weight tile is copied into one of three
+// LDS buffers two steps ahead (issued in step t-2), and the activations are
+// loaded into registers two steps ahead (issued in step t-2, split and written
+// to one of two LDS buffers at the start of step t-1). Step t writes the
+// activations of tile t+1, issues the loads of tile t+2, runs the 16 MFMAs of
+// tile t per wave, then waits for everything but the loads it just issued.
 __global__ __launch_bounds__(256, 2) void linear_gemm_kernel(const LinearArgs a) {
   __shared__ __attribute__((aligned(1024))) char w_lds0[kBN * kRowBytes];
   __shared__ __attribute__((aligned(1024))) char w_lds1[kBN * kRowBytes];
+  __shared__ __attribute__((aligned(1024))) char w_lds2[kBN * kRowBytes];
   __shared__ __attribute__((aligned(1024))) char xh_lds0[kBM * kRowBytes];
   __shared__ __attribute__((aligned(1024))) char xh_lds1[kBM * kRowBytes];
   __shared__ __attribute__((aligned(1024))) char xl_lds0[kBM * kRowBytes];
@@ -212,22 +228,21 @@ __global__ __launch_bounds__(256, 2) void linear_gemm_kernel(const LinearArgs a)
   // and 2 (t % 2) + 1 of the row).
   const int xr = tid >> 1, xc = tid & 1;
   const float *xg = a.x + (long)min(m0 + xr, a.M - 1) * a.K + 16 * xc;
-  float4 xv[4];
-  auto load_x = [&](int kt) {
+  auto load_x = [&](int kt, float4 (&xv)[4]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) xv[i] = *reinterpret_cast<const float4 *>(xg + (long)kt * kBK + 4 * i);
   };
-  auto store_x = [&](char *hi, char *lo) {
+  auto store_x = [&](const float4 (&xv)[4], char *hi, char *lo) {
     const float f[16] = {xv[0].x, xv[0].y, xv[0].z, xv[0].w, xv[1].x, xv[1].y, xv[1].z, xv[1].w,
                          xv[2].x, xv[2].y, xv[2].z, xv[2].w, xv[3].x, xv[3].y, xv[3].z, xv[3].w};
     unsigned h[8], l[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const unsigned short h0 = bf16_rne_bits(f[2 * i]), h1 = bf16_rne_bits(f[2 * i + 1]);
-      const float r0 = f[2 * i] - __uint_as_float((unsigned)h0 << 16);
-      const float r1 = f[2 * i + 1] - __uint_as_float((unsigned)h1 << 16);
-      h[i] = (unsigned)h0 | ((unsigned)h1 << 16);
-      l[i] = (unsigned)bf16_rne_bits(r0) | ((unsigned)bf16_rne_bits(r1) << 16);
+      // one v_cvt_pk_bf16_f32 per pair (round to nearest even), for hi and for lo
+      h[i] = bf16x2_rne(f[2 * i], f[2 * i + 1]);
+      const float r0 = f[2 * i] - __uint_as_float(h[i] << 16);
+      const float r1 = f[2 * i + 1] - __uint_as_float(h[i] & 0xffff0000u);
+      l[i] = bf16x2_rne(r0, r1);
     }
 #pragma unroll
     for (int cc = 0; cc < 2; ++cc) {
@@ -278,34 +293,57 @@ __global__ __launch_bounds__(256, 2) void linear_gemm_kernel(const LinearArgs a)
     }
   };
 
-  // Prologue: tile 0 into buffer 0.
+  // One step on tile t; W selects the weight buffers (t % 3 computes, (t+2) % 3
+  // receives), X the activation buffers (t % 2 computes, (t+1) % 2 receives),
+  // xnext holds tile t+1's activations and receives tile t+2's.
+  auto step = [&](auto W_, auto X_, int t, float4 (&xnext)[4]) {
+    constexpr int W = decltype(W_)::value, X = decltype(X_)::value;
+    char *const w_cur = W == 0 ? w_lds0 : W == 1 ? w_lds1 : w_lds2;
+    char *const w_fill = W == 0 ? w_lds2 : W == 1 ? w_lds0 : w_lds1;
+    char *const xh_cur = X ? xh_lds1 : xh_lds0, *const xl_cur = X ? xl_lds1 : xl_lds0;
+    char *const xh_fill = X ? xh_lds0 : xh_lds1, *const xl_fill = X ? xl_lds0 : xl_lds1;
+    if (t + 1 < nk) store_x(xnext, xh_fill, xl_fill);
+    const bool more = t + 2 < nk;
+    if (more) {
+      copy_w(t + 2, w_fill);
+      load_x(t + 2, xnext);
+    }
+    compute(w_cur, xh_cur, xl_cur);
+    // all loads but this step's (2 weight copies + 4 activation loads) are done
+    if (more) __builtin_amdgcn_s_waitcnt(0x0F76);  // vmcnt(6)
+    else __builtin_amdgcn_s_waitcnt(0x0F70);       // vmcnt(0)
+    __syncthreads();
+  };
+
+  // Prologue: weights of tiles 0 and 1 copied, activations of tile 0 in LDS,
+  // tile 1's in registers.
+  float4 xv[4];
   copy_w(0, w_lds0);
-  load_x(0);
-  store_x(xh_lds0, xl_lds0);
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's weight copies
+  if (nk > 1) copy_w(1, w_lds1);
+  load_x(0, xv);
+  store_x(xv, xh_lds0, xl_lds0);
+  if (nk > 1) load_x(1, xv);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   __syncthreads();
 
-  for (int kt = 0; kt < nk; kt += 2) {
-    // even step: compute buffer 0, fill buffer 1
-    if (kt + 1 < nk) {
-      copy_w(kt + 1, w_lds1);
-      load_x(kt + 1);
-    }
-    compute(w_lds0, xh_lds0, xl_lds0);
-    if (kt + 1 < nk) store_x(xh_lds1, xl_lds1);
-    __builtin_amdgcn_s_waitcnt(0x0F70);
-    __syncthreads();
-    if (kt + 1 >= nk) break;
-    // odd step: compute buffer 1, fill buffer 0
-    if (kt + 2 < nk) {
-      copy_w(kt + 2, w_lds0);
-      load_x(kt + 2);
-    }
-    compute(w_lds1, xh_lds1, xl_lds1);
-    if (kt + 2 < nk) store_x(xh_lds0, xl_lds0);
-    __builtin_amdgcn_s_waitcnt(0x0F70);
-    __syncthreads();
+  // The buffer pattern repeats every 6 tiles.
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  int t = 0;
+  for (; t + 6 <= nk; t += 6) {
+    step(I0(), I0(), t, xv);
+    step(I1(), I1(), t + 1, xv);
+    step(I2(), I0(), t + 2, xv);
+    step(I0(), I1(), t + 3, xv);
+    step(I1(), I0(), t + 4, xv);
+    step(I2(), I1(), t + 5, xv);
   }
+  if (t < nk) step(I0(), I0(), t, xv);
+  if (t + 1 < nk) step(I1(), I1(), t + 1, xv);
+  if (t + 2 < nk) step(I2(), I0(), t + 2, xv);
+  if (t + 3 < nk) step(I0(), I1(), t + 3, xv);
+  if (t + 4 < nk) step(I1(), I0(), t + 4, xv);
 
   // Accumulator layout: element e of lane l is row 8 (e / 4) + 4 hl + e % 4,
   // column lr of its 32 x 32 block.
@@ -321,6 +359,81 @@ __global__ __launch_bounds__(256, 2) void linear_gemm_kernel(const LinearArgs a)
         const int m = m0 + wm * 64 + 32 * i + 8 * (e >> 2) + 4 * hl + (e & 3);
         if (m < a.M) a.out[(long)m * a.N + n] = bn + acc[i][j][e];
       }
+  }
+}
+
+namespace {
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+constexpr int kSkinnyRows = 16;  // weight rows (output features) per workgroup
+}  // namespace
+
+// Grid: ceil(N / 16) workgroups of 256 threads, for 5..64 tokens (MB blocks
+// of 16), bf16 weights, K % 128 == 0. Wave w covers k in [w K/4, (w+1) K/4).
+// Per 32-deep k step a lane loads 16 bytes of one weight row (the A operand
+// of v_mfma_f32_16x16x32_bf16: row lane % 16, k 8 (lane / 16) + [0, 8)) straight
+// from HBM, and 8 activations of one token (the B operand) from the cache,
+// split into bf16 hi and lo; both meet the weights. The four waves' partial
+// sums are added through LDS.
+template <int MB>
+__global__ __launch_bounds__(256) void linear_skinny_kernel(const LinearArgs a) {
+  __shared__ f32x4 part[4][MB][64];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int n0 = blockIdx.x * kSkinnyRows;
+  const int r = lane & 15, kq = lane >> 4;  // operand row/column, k quarter (8 of 32)
+  const int kw = a.K / 4;
+  const int k_begin = wave * kw, k_end = k_begin + kw;
+  const char *wrow = reinterpret_cast<const char *>(a.w) + (long)min(n0 + r, a.N - 1) * a.K * 2;
+  const float *xrow[MB];
+#pragma unroll
+  for (int b = 0; b < MB; ++b) xrow[b] = a.x + (long)min(16 * b + r, a.M - 1) * a.K;
+
+  f32x4 acc[MB];
+#pragma unroll
+  for (int b = 0; b < MB; ++b) acc[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto step = [&](int kk) {
+    const bf16x8 wf = *reinterpret_cast<const bf16x8 *>(wrow + (long)(kk + 8 * kq) * 2);
+#pragma unroll
+    for (int b = 0; b < MB; ++b) {
+      const float4 x0 = *reinterpret_cast<const float4 *>(xrow[b] + kk + 8 * kq);
+      const float4 x1 = *reinterpret_cast<const float4 *>(xrow[b] + kk + 8 * kq + 4);
+      const float f[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+      unsigned h[4], l[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        h[i] = bf16x2_rne(f[2 * i], f[2 * i + 1]);
+        l[i] = bf16x2_rne(f[2 * i] - __uint_as_float(h[i] << 16), f[2 * i + 1] - __uint_as_float(h[i] & 0xffff0000u));
+      }
+      const bf16x8 xh = __builtin_bit_cast(bf16x8, make_uint4(h[0], h[1], h[2], h[3]));
+      const bf16x8 xl = __builtin_bit_cast(bf16x8, make_uint4(l[0], l[1], l[2], l[3]));
+      acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf, xh, acc[b], 0, 0, 0);
+      acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf, xl, acc[b], 0, 0, 0);
+    }
+  };
+  constexpr int U = MB <= 2 ? 8 : 4;  // k steps in flight (registers allowing)
+  int kk = k_begin;
+  for (; kk + 32 * U <= k_end; kk += 32 * U) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) step(kk + 32 * u);
+  }
+  for (; kk < k_end; kk += 32) step(kk);
+
+#pragma unroll
+  for (int b = 0; b < MB; ++b) part[wave][b][lane] = acc[b];
+  __syncthreads();
+  // D layout: element e of lane l is row (weight) 4 (l / 16) + e, column
+  // (token) l % 16 of its block. Thread t < 64 * MB finishes block t / 64.
+  if (threadIdx.x < 64 * MB) {
+    const int b = threadIdx.x >> 6, l = threadIdx.x & 63;
+    const f32x4 s = part[0][b][l] + part[1][b][l] + part[2][b][l] + part[3][b][l];
+    const int t = 16 * b + (l & 15);
+    if (t < a.M) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int n = n0 + 4 * (l >> 4) + e;
+        if (n < a.N) a.out[(long)t * a.N + n] = (a.bias ? a.bias[n] : 0.0f) + s[e];
+      }
+    }
   }
 }
 
@@ -375,6 +488,7 @@ hipError_t launch_typed(hipStream_t st, const LinearArgs &a, int path) {
 
 int linear_path(int dtype, long M, long K) {
   const int epc = dtype == SPISSA_DTYPE_F32 ? 4 : 8;
+  if (dtype == SPISSA_DTYPE_BF16 && M > 4 && M <= 64 && K % 128 == 0) return kLinearSkinny;
   if (dtype == SPISSA_DTYPE_BF16 && M > 4 && K % kBK == 0) return kLinearGemm;
   if (M <= 4 && K % epc == 0) return kLinearGemv;
   return kLinearGeneric;
@@ -382,6 +496,17 @@ int linear_path(int dtype, long M, long K) {
 
 hipError_t launch_linear(hipStream_t st, const LinearArgs &a, int path) {
   if (a.M <= 0 || a.N <= 0) return hipSuccess;
+  if (path == kLinearSkinny) {
+    if (a.dtype != SPISSA_DTYPE_BF16 || a.K % 128 != 0 || a.M > 64) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((a.N + kSkinnyRows - 1) / kSkinnyRows));
+    switch ((a.M + 15) / 16) {
+      case 1: hipLaunchKernelGGL(linear_skinny_kernel<1>, grid, dim3(256), 0, st, a); break;
+      case 2: hipLaunchKernelGGL(linear_skinny_kernel<2>, grid, dim3(256), 0, st, a); break;
+      case 3: hipLaunchKernelGGL(linear_skinny_kernel<3>, grid, dim3(256), 0, st, a); break;
+      default: hipLaunchKernelGGL(linear_skinny_kernel<4>, grid, dim3(256), 0, st, a); break;
+    }
+    return hipGetLastError();
+  }
   if (path == kLinearGemm) {
     if (a.dtype != SPISSA_DTYPE_BF16 || a.K % kBK != 0) return hipErrorInvalidValue;
     const long grid = (long)((a.M + kBM - 1) / kBM) * ((a.N + kBN - 1) / kBN);
