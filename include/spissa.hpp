@@ -1,6 +1,7 @@
 // spissa.hpp -- C++17 mirror of the Spissa runtime's attention API
-// (crates/spissa-runtime/src/rotary.rs, ops.rs, models/gemma/model.rs) over
-// the C ABI of spissa_hip.h. Header-only; link with libspissa_hip.so.
+// (crates/spissa-runtime/src/rotary.rs, ops.rs, models/gemma/model.rs) and of
+// the streaming linear projections either side of it (streaming/linear.rs)
+// over the C ABI of spissa_hip.h. Header-only; link with libspissa_hip.so.
 //
 // The names, argument order and meaning follow the Rust functions they
 // replace, so code (and tests) written against the reference read the same:
@@ -11,6 +12,7 @@
 //   KvCache::new(h, d, max)                    spissa::KvCache::create(h, d, max)
 //   Option<&KvCache>                           const spissa::KvCache* (nullptr = None)
 //   Option<&[f32]>                             const std::vector<float>* (nullptr = None)
+//   LazySpissaModel + weight name              spissa::LinearModel (resident weights by name)
 // Errors are returned, never thrown; Result<T>::unwrap() throws
 // std::runtime_error for callers that prefer exceptions (as .unwrap() panics).
 // The drop-in calls copy host buffers to the device and back and return when
@@ -19,6 +21,7 @@
 #pragma once
 
 #include <cstddef>
+#include <map>
 #include <stdexcept>
 #include <string>
 #include <type_traits>
@@ -31,8 +34,8 @@ namespace spissa {
 
 // crates/spissa-runtime/src/error.rs:6-54, the variants this path returns
 // (Device and Argument have no reference counterpart: HIP failures and null
-// handles).
-enum class ErrorKind { Shape, InvalidTensorData, Device, Argument };
+// handles; MissingTensor is lazy.rs:357-361).
+enum class ErrorKind { Shape, InvalidTensorData, Device, Argument, MissingTensor };
 
 struct RuntimeError {
   ErrorKind kind;
@@ -44,6 +47,7 @@ inline const char *kind_name(ErrorKind k) {
     case ErrorKind::Shape: return "Shape";
     case ErrorKind::InvalidTensorData: return "InvalidTensorData";
     case ErrorKind::Device: return "Device";
+    case ErrorKind::MissingTensor: return "MissingTensor";
     default: return "Argument";
   }
 }
@@ -288,6 +292,96 @@ inline bool is_global_layer(size_t layer_idx, size_t sliding_window_pattern) {
   return spissa_is_global_layer(layer_idx, sliding_window_pattern) != 0;
 }
 
+// ---- linear projections (streaming/linear.rs:269-576) ----
+
+enum class DType { F32 = SPISSA_DTYPE_F32, F16 = SPISSA_DTYPE_F16, Bf16 = SPISSA_DTYPE_BF16 };
+
+// streaming/mod.rs:511-516
+struct StreamingLinearConfig {
+  size_t batch;
+  size_t in_features;
+  size_t out_features;
+  spissa_linear_config c() const { return spissa_linear_config{batch, in_features, out_features}; }
+};
+
+// streaming/mod.rs:518-526. tile_elements bounds the reference's f32 CPU
+// scratch; the device path has none, so it is only validated (> 0).
+struct StreamingTileLinearConfig {
+  StreamingLinearConfig linear;
+  size_t tile_elements;
+};
+
+class Session;
+
+// A [out_features, in_features] row-major weight resident in HBM, uploaded
+// from its raw little-endian element bytes. Free it before its session.
+class LinearWeight {
+ public:
+  // session = nullptr: the calling thread's default session.
+  static Result<LinearWeight> create(DType dtype, size_t out_features, size_t in_features, const void *data,
+                                     size_t data_bytes, const Session *session = nullptr);
+  LinearWeight() = default;
+  LinearWeight(LinearWeight &&o) noexcept : w_(o.w_) { o.w_ = nullptr; }
+  LinearWeight &operator=(LinearWeight &&o) noexcept {
+    if (this != &o) {
+      if (w_) spissa_linear_weight_free(w_);
+      w_ = o.w_;
+      o.w_ = nullptr;
+    }
+    return *this;
+  }
+  LinearWeight(const LinearWeight &) = delete;
+  LinearWeight &operator=(const LinearWeight &) = delete;
+  ~LinearWeight() {
+    if (w_) spissa_linear_weight_free(w_);
+  }
+  spissa_linear_weight *raw() const { return w_; }
+
+ private:
+  explicit LinearWeight(spissa_linear_weight *w) : w_(w) {}
+  spissa_linear_weight *w_ = nullptr;
+};
+
+// Resident weights by tensor name: the role of lazy.rs's LazySpissaModel.
+class LinearModel {
+ public:
+  void add(const std::string &name, LinearWeight w) { w_[name] = std::move(w); }
+  // lazy.rs:357-361
+  Result<const LinearWeight *> tensor(const std::string &name) const {
+    auto it = w_.find(name);
+    if (it == w_.end()) return RuntimeError{ErrorKind::MissingTensor, name};
+    return &it->second;
+  }
+
+ private:
+  std::map<std::string, LinearWeight> w_;
+};
+
+// input[batch, in] x W^T + bias on the GPU (ops.rs:62-105 arithmetic in f32);
+// bias = nullptr is Option::None. Shape errors as streaming/validation.rs:225-289.
+inline Result<std::vector<float>> linear(const LinearWeight &w, Slice<const float> input,
+                                         const std::vector<float> *bias, const StreamingLinearConfig &config) {
+  std::vector<float> out(config.batch * config.out_features);
+  const auto c = config.c();
+  auto r = detail::check(spissa_linear(w.raw(), input.ptr, input.len, bias ? bias->data() : nullptr,
+                                       bias ? bias->size() : 0, &c, out.data(), out.size()));
+  if (r.is_err()) return r.error();
+  return out;
+}
+
+// streaming/linear.rs:269-576 with the weight already resident.
+inline Result<std::vector<float>> streaming_tile_linear_from_model(const LinearModel &model,
+                                                                   const std::string &weight_name,
+                                                                   Slice<const float> input,
+                                                                   const std::vector<float> *bias,
+                                                                   const StreamingTileLinearConfig &config) {
+  if (config.tile_elements == 0)  // streaming/validation.rs:249-256
+    return RuntimeError{ErrorKind::Shape, "tile_elements must be greater than zero"};
+  auto w = model.tensor(weight_name);
+  if (w.is_err()) return w.error();
+  return linear(*w.value(), input, bias, config.linear);
+}
+
 // ---- device tier (no reference counterpart): device pointers, one stream ----
 
 enum class RopeKind { Llama = SPISSA_ROPE_LLAMA, Gemma = SPISSA_ROPE_GEMMA, Neox = SPISSA_ROPE_NEOX };
@@ -405,6 +499,15 @@ class Session {
     return detail::check(
         spissa_attention_decode_batch_device(s_, d_q, d_k, d_v, raw.data(), raw.size(), &c, d_out));
   }
+  // out[batch, out] = x[batch, in] x W^T + bias on device buffers (d_bias may be null).
+  Result<void> linear(const LinearWeight &w, const float *d_x, const float *d_bias, size_t batch,
+                      float *d_out) const {
+    return detail::check(spissa_linear_device(s_, w.raw(), d_x, d_bias, batch, d_out));
+  }
+  Result<LinearWeight> linear_weight(DType dtype, size_t out_features, size_t in_features, const void *data,
+                                     size_t data_bytes) const {
+    return LinearWeight::create(dtype, out_features, in_features, data, data_bytes, this);
+  }
   // RoPE + attention + append of one decode step of one layer (table = nullptr: no RoPE).
   Result<void> decode_step(const RopeTable *table, const float *d_q, const float *d_k, const float *d_v,
                            const std::vector<KvCache *> &caches, const KvAttentionConfig &cfg, float *d_out) const {
@@ -419,5 +522,21 @@ class Session {
   explicit Session(spissa_session *s) : s_(s) {}
   spissa_session *s_ = nullptr;
 };
+
+inline Result<LinearWeight> LinearWeight::create(DType dtype, size_t out_features, size_t in_features,
+                                                 const void *data, size_t data_bytes, const Session *session) {
+  spissa_session *s = nullptr;
+  if (session) {
+    s = session->raw();
+  } else {
+    auto r = detail::check(spissa_default_session(&s));
+    if (r.is_err()) return r.error();
+  }
+  spissa_linear_weight *w = nullptr;
+  auto r = detail::check(
+      spissa_linear_weight_new(s, static_cast<int>(dtype), out_features, in_features, data, data_bytes, &w));
+  if (r.is_err()) return r.error();
+  return LinearWeight(w);
+}
 
 }  // namespace spissa

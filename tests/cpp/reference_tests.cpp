@@ -13,6 +13,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <cmath>
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <functional>
@@ -379,6 +380,62 @@ TEST(session_append_rolls_back_all_caches_after_a_later_layer_fails) {
   ok(layer0.truncate(before));
   CHECK(layer0.len() == 0 && layer0.is_empty() && layer0.resident_bytes() == 0);
   CHECK(layer1.len() == 0);
+}
+
+// --------------------------------------------------------- streaming linear
+
+// streaming/tests.rs:2128-2181 (raw bf16 batch 1) and 2078-2125 (raw fp16):
+// the same 4x3 weight, input [1.5, -2, 0.25], bias; every product and partial
+// sum is exact in f32, so the expected values are exact.
+static void linear_kat(DType dtype, const std::vector<uint16_t> &bits) {
+  LinearModel model;
+  model.add("linear.batch1.weight", ok(LinearWeight::create(dtype, 4, 3, bits.data(), bits.size() * 2)));
+  const std::vector<float> input{1.5f, -2.0f, 0.25f}, bias{0.0f, 0.5f, -1.0f, 4.0f};
+  auto actual = ok(streaming_tile_linear_from_model(model, "linear.batch1.weight", input, &bias,
+                                                    StreamingTileLinearConfig{StreamingLinearConfig{1, 3, 4}, 2}));
+  assert_close_vec(actual, {3.25f, -2.875f, -1.75f, 5.1875f}, 1e-6f);
+}
+TEST(streaming_tile_linear_uses_raw_bf16_batch1_path) {
+  linear_kat(DType::Bf16, {0x3f00, 0xbf80, 0x4000, 0xc000, 0x3e80, 0x3f00, 0x3f80, 0x3f80, 0xbf80, 0x0000, 0xbf00,
+                           0x3f40});
+}
+TEST(streaming_tile_linear_matches_raw_fp16_batch1_linear) {
+  linear_kat(DType::F16, {0x3800, 0xbc00, 0x4000, 0xc000, 0x3400, 0x3800, 0x3c00, 0x3c00, 0xbc00, 0x0000, 0xb800,
+                          0x3a00});
+}
+
+// ops.rs:488-495 through the device linear with f32 weights
+TEST(linear_uses_transposed_weight_layout) {
+  const std::vector<float> weight{1.0, 0.0, 1.0, 0.5, 0.5, 0.5}, bias{1.0, -1.0};
+  auto w = ok(LinearWeight::create(DType::F32, 2, 3, weight.data(), weight.size() * 4));
+  auto out = ok(linear(w, std::vector<float>{1.0f, 2.0f, 3.0f}, &bias, StreamingLinearConfig{1, 3, 2}));
+  CHECK(out == (std::vector<float>{5.0f, 2.0f}));
+}
+
+// streaming/validation.rs:225-256 and lazy.rs:357-361: errors before any work
+HOST_TEST(streaming_tile_linear_rejects_zero_tile_and_missing_tensor) {
+  LinearModel model;
+  const std::vector<float> input{1.0f, 2.0f, 3.0f};
+  auto zero = streaming_tile_linear_from_model(model, "w", input, nullptr,
+                                               StreamingTileLinearConfig{StreamingLinearConfig{1, 3, 2}, 0});
+  CHECK(zero.is_err() && zero.error().kind == ErrorKind::Shape);
+  auto missing = streaming_tile_linear_from_model(model, "w", input, nullptr,
+                                                  StreamingTileLinearConfig{StreamingLinearConfig{1, 3, 2}, 4});
+  CHECK(missing.is_err() && missing.error().kind == ErrorKind::MissingTensor);
+}
+
+TEST(linear_rejects_mismatched_shapes_and_bytes) {
+  const std::vector<float> weight(6, 0.0f);
+  auto w = ok(LinearWeight::create(DType::F32, 2, 3, weight.data(), weight.size() * 4));
+  auto bad_input = linear(w, std::vector<float>(4, 1.0f), nullptr, StreamingLinearConfig{1, 3, 2});
+  CHECK(bad_input.is_err() && bad_input.error().kind == ErrorKind::Shape);
+  const std::vector<float> bias3(3, 0.0f);
+  auto bad_bias = linear(w, std::vector<float>(3, 1.0f), &bias3, StreamingLinearConfig{1, 3, 2});
+  CHECK(bad_bias.is_err() && bad_bias.error().kind == ErrorKind::Shape);
+  auto bad_shape = linear(w, std::vector<float>(2, 1.0f), nullptr, StreamingLinearConfig{1, 2, 3});
+  CHECK(bad_shape.is_err() && bad_shape.error().kind == ErrorKind::Shape);
+  auto bad_bytes = LinearWeight::create(DType::F32, 2, 3, weight.data(), 5 * 4);
+  CHECK(bad_bytes.is_err() && bad_bytes.error().kind == ErrorKind::InvalidTensorData);
 }
 
 // --------------------------------------------------- ABI contract (no Rust test)
