@@ -386,6 +386,20 @@ def cpu_baseline(args) -> dict:
         out["prefill"] = {
             "TFLOPs": prefill_flops(n) / t_layer / 1e12, "us_per_layer": t_layer * 1e6, "cores": 1,
             "sample": f"last 128 query rows of a 4096-token layer ({ts:.2f} s), x{scale:.1f} by operation count"}
+        # The fused q/k/v projection at decode batch 1 (ops.rs linear over the
+        # bf16 weight): 5120 x 3072 multiply-adds, single thread.
+        hid, qkv = HQ * D, (HQ + 2 * HKV) * D
+        wbits = (normal_f32(seed_for(3, 0, 2, "k"), qkv * hid, 0.0, 0.02).view(np.uint32) >> 16).astype(np.uint16)
+        x = normal_f32(seed_for(3, 0, 2, "q"), hid)
+        lt = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            oracle.linear(x, wbits, oracle.DTYPE_BF16, None, 1, hid, qkv)
+            lt.append(time.perf_counter() - t0)
+        tl = statistics.median(lt)
+        out["projection_b1"] = {
+            "value": qkv * hid * 2 / tl / 1e9, "unit": "GB/s of weights", "us_per_layer": tl * 1e6, "cores": 1,
+            "sample": "oracle linear, Llama-3.2-3B fused q/k/v weight (5120 x 3072 bf16), batch 1, median of 3"}
     return out
 
 
