@@ -192,6 +192,12 @@ def gpu_bench(args) -> dict:
         }
         del g_step, g_attn
 
+        # ---- the whole attention sublayer at decode, batch 1 ----
+        if not args.decode_only:
+            log("timing the decode attention sublayer")
+            res["sublayer_b1"] = sublayer_bench(sess, stream, dev, gen, caches, table, reset_lengths,
+                                                time_graph, args)
+
         if args.copy_probe:
             # A plain copy of known size: 256 MiB read + 256 MiB written per launch.
             src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
@@ -281,6 +287,56 @@ def gpu_bench(args) -> dict:
             log("timing projections")
             res["projections"] = projection_bench(sess, stream, gen, dev, args, time_graph)
     return res
+
+
+def sublayer_bench(sess, stream, dev, gen, caches, table, reset_lengths, time_graph, args) -> dict:
+    """One Llama-3.2-3B attention sublayer per layer at decode batch 1, over
+    the 8192-token caches: input RMSNorm, q/k/v projections (bf16 weights),
+    RoPE + attention + append (the fused decode step), o projection."""
+    import numpy as np
+    import torch
+
+    from spissa_amd.device import AttentionLayer
+    from spissa_amd.linear import DTYPE_BF16
+
+    hid = HQ * D
+    rng = np.random.default_rng(12)
+
+    def bits(n):
+        return ((rng.standard_normal(n).astype(np.float32) * 0.02).view(np.uint32) >> 16).astype(np.uint16)
+
+    hq, hkv, ho = bits(hid * hid), bits(HKV * D * hid), bits(hid * hid)
+    layers = []
+    for l in range(LAYERS):
+        wq = sess.linear_weight(hq, DTYPE_BF16, hid, hid)
+        wk = sess.linear_weight(hkv, DTYPE_BF16, HKV * D, hid)
+        wv = sess.linear_weight(hkv, DTYPE_BF16, HKV * D, hid)
+        wo = sess.linear_weight(ho, DTYPE_BF16, hid, hid)
+        with torch.cuda.stream(stream):
+            norm = 1.0 + 0.1 * torch.randn(hid, generator=gen, device=dev)
+        layers.append(AttentionLayer(hid, HQ, HKV, D, wq, wk, wv, wo, input_norm=norm, eps=1e-5, rope=table))
+    with torch.cuda.stream(stream):
+        xs = [torch.randn(hid, generator=gen, device=dev) for _ in range(LAYERS)]
+        ys = [torch.empty(hid, device=dev) for _ in range(LAYERS)]
+
+    def step():
+        for l in range(LAYERS):
+            sess.attention_sublayer(layers[l], xs[l], 1, caches[l], ys[l])
+
+    reset_lengths()
+    step()  # sizes the workspace before capture
+    sess.sync()
+    reset_lengths()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        step()
+    reset_lengths()
+    ms = time_graph(g, args.steps, args.warmup)
+    wbytes = 2 * (2 * hid * hid + 2 * HKV * D * hid)
+    per_layer = wbytes + decode_bytes(CTX + 1)
+    del g, layers
+    return {"us_per_layer": ms * 1e3 / LAYERS, "bytes_per_layer": per_layer,
+            "GBps": LAYERS * per_layer / (ms * 1e-3) / 1e9, "tokens_per_s": 1e3 / ms}
 
 
 def projection_bench(sess, stream, gen, dev, args, time_graph) -> dict:
@@ -464,6 +520,11 @@ def main() -> int:
         line["roofline_prefill"] = {"bound": "mfma", "achieved": round(p["TFLOPs"], 2), "peak": BF16_PEAK_TFLOPS,
                                     "unit": "TFLOP/s", "frac": round(p["TFLOPs"] / BF16_PEAK_TFLOPS, 4),
                                     "dtype": "bf16 MFMA, f32 accumulate"}
+    if "sublayer_b1" in res:
+        line["sublayer_b1"] = {"workload": "llama-3.2-3B attention sublayer at decode, batch 1, 8192-token "
+                                           "cache: input RMSNorm, q/k/v projections (bf16), RoPE + attention "
+                                           "+ append, o projection",
+                               **{k: round(v, 3) for k, v in res["sublayer_b1"].items()}}
     if "projections" in res:
         line["projections"] = {"workload": "llama-3.2-3B fused q/k/v projection, 5120 x 3072 bf16 weight "
                                            "resident in HBM, f32 activations and output",

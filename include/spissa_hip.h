@@ -52,6 +52,8 @@ typedef struct spissa_session spissa_session;
 
 /* stream: an existing hipStream_t to run on (not owned), or NULL to create one. */
 int spissa_session_create(int device, void *stream, spissa_session **out);
+/* Releases the caller's session; its memory goes when the last cache and
+ * weight created on it have been freed too (they hold references). */
 void spissa_session_destroy(spissa_session *s);
 int spissa_default_session(spissa_session **out);
 /* Wait for all work of the session; returns INVALID_TENSOR_DATA if a device
@@ -243,8 +245,7 @@ typedef struct spissa_linear_weight spissa_linear_weight;
  * (streaming/validation.rs:258-289: InvalidTensorData otherwise). */
 int spissa_linear_weight_new(spissa_session *s, int dtype, size_t out_features, size_t in_features,
                              const void *data, size_t data_bytes, spissa_linear_weight **out);
-/* Frees the weight after the work queued on its session; call it before the
- * session is destroyed. */
+/* Frees the weight after the work queued on its session. */
 void spissa_linear_weight_free(spissa_linear_weight *w);
 /* streaming/mod.rs:511-516 StreamingLinearConfig */
 typedef struct {
@@ -263,6 +264,40 @@ int spissa_linear(const spissa_linear_weight *w, const float *input, size_t inpu
  * d_out [batch, out]), asynchronous on the session stream. */
 int spissa_linear_device(spissa_session *s, const spissa_linear_weight *w, const float *d_input,
                          const float *d_bias, size_t batch, float *d_out);
+
+/* ------------------------------------------------------------------------ */
+/* The attention sublayer of one layer on the device, in the reference's    */
+/* order (models/gemma/generate.rs:178-312, models/llama/generate.rs:200-450): */
+/* input RMSNorm, q/k/v projections, QK-norm (Gemma), RoPE at the cache's    */
+/* next positions, q prescale, attention over cache + current rows, append   */
+/* of the rotated k and v, o projection, post-attention RMSNorm (Gemma).     */
+/* ------------------------------------------------------------------------ */
+typedef struct {
+    size_t hidden;
+    size_t q_heads;
+    size_t kv_heads;
+    size_t head_dim;
+    const spissa_linear_weight *q_weight; /* [q_heads * head_dim, hidden] */
+    const spissa_linear_weight *k_weight; /* [kv_heads * head_dim, hidden] */
+    const spissa_linear_weight *v_weight; /* [kv_heads * head_dim, hidden] */
+    const spissa_linear_weight *o_weight; /* [hidden, q_heads * head_dim] */
+    const float *d_input_norm;  /* [hidden] RMSNorm multipliers (Gemma's 1 + w), or NULL: none */
+    const float *d_q_norm;      /* [head_dim] QK-norm multipliers, or NULL (then d_k_norm too) */
+    const float *d_k_norm;
+    const float *d_post_norm;   /* [hidden] post-attention RMSNorm multipliers, or NULL */
+    float eps;                  /* RMSNorm epsilon of all the norms */
+    const spissa_rope_table *rope; /* the layer's LLAMA or GEMMA table over the whole head, or NULL */
+    float q_prescale;           /* models/gemma/generate.rs:275; must be 1 without the QK-norm */
+    int causal;
+    size_t window;              /* sliding window (0: none) */
+} spissa_attention_layer;
+/* d_x [seq_len, hidden] -> d_out [seq_len, hidden], asynchronous on the
+ * session stream. RoPE positions start at the cache's length (0 without a
+ * cache); with a cache the rotated k and v are appended, which must fit. The
+ * cache must belong to the session. All checks run before any launch. */
+int spissa_attention_sublayer_device(spissa_session *s, const spissa_attention_layer *layer,
+                                     const float *d_x, size_t seq_len, spissa_kv_cache *cache,
+                                     float *d_out);
 
 /* Prefill arithmetic for query_len > 1: SPISSA_PREFILL_BF16 (default) runs
  * the MFMA kernel; SPISSA_PREFILL_F32 runs the f32 SIMT kernel. */

@@ -39,6 +39,18 @@ class LinearConfigC(C.Structure):
     _fields_ = [("batch", c_size), ("in_features", c_size), ("out_features", c_size)]
 
 
+class AttentionLayerC(C.Structure):
+    """spissa_attention_layer (models/gemma/generate.rs:178-312)."""
+
+    _fields_ = [
+        ("hidden", c_size), ("q_heads", c_size), ("kv_heads", c_size), ("head_dim", c_size),
+        ("q_weight", c_void_p), ("k_weight", c_void_p), ("v_weight", c_void_p), ("o_weight", c_void_p),
+        ("d_input_norm", c_void_p), ("d_q_norm", c_void_p), ("d_k_norm", c_void_p), ("d_post_norm", c_void_p),
+        ("eps", C.c_float), ("rope", c_void_p), ("q_prescale", C.c_float), ("causal", C.c_int),
+        ("window", c_size),
+    ]
+
+
 class RotaryConfigC(C.Structure):
     """spissa_rotary_config (rotary.rs:6-14)."""
 
@@ -146,6 +158,8 @@ SIGNATURES = {
         C.c_int, [c_void_p, c_float_p, c_size, c_float_p, c_size, C.POINTER(LinearConfigC), c_float_p,
                   c_size]),
     "spissa_linear_device": (C.c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size, c_void_p]),
+    "spissa_attention_sublayer_device": (
+        C.c_int, [c_void_p, C.POINTER(AttentionLayerC), c_void_p, c_size, c_void_p, c_void_p]),
 }
 
 _lib = None

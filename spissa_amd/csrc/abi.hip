@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -77,12 +78,17 @@ struct spissa_session {
   DevBuf stage;     // prefill bf16 staging of K / V^T
   DevBuf table;     // drop-in RoPE rows
   DevBuf ppart;     // prefill key-split partials (O, then (m, l))
+  DevBuf sub;       // attention sublayer intermediates (normed x, q, k, v, attention, projection)
   int cus = 256;    // compute units of the device
   // Buffers replaced by larger ones. They stay allocated until the session
   // is destroyed, so a HIP graph captured before a workspace grew still
   // replays on valid memory.
   std::vector<void *> retired;
   int prefill_precision = SPISSA_PREFILL_BF16;
+  // The owner's reference plus one per cache and weight created on the
+  // session: those are freed through it, so it outlives them whatever order
+  // the caller releases things in.
+  std::atomic<int> refs{1};
 };
 
 struct spissa_kv_cache {
@@ -151,8 +157,7 @@ extern "C" int spissa_session_create(int device, void *stream, spissa_session **
   GUARD_END
 }
 
-extern "C" void spissa_session_destroy(spissa_session *s) {
-  if (!s) return;
+static void session_free(spissa_session *s) {
   (void)hipSetDevice(s->device);
   (void)hipStreamSynchronize(s->stream);
   free_buf(s->io);
@@ -160,10 +165,21 @@ extern "C" void spissa_session_destroy(spissa_session *s) {
   free_buf(s->stage);
   free_buf(s->table);
   free_buf(s->ppart);
+  free_buf(s->sub);
   for (void *p : s->retired) (void)hipFree(p);
   if (s->d_err) (void)hipFree(s->d_err);
   if (s->own_stream) (void)hipStreamDestroy(s->stream);
   delete s;
+}
+
+static void session_retain(spissa_session *s) { s->refs.fetch_add(1, std::memory_order_relaxed); }
+static void session_release(spissa_session *s) {
+  if (s->refs.fetch_sub(1, std::memory_order_acq_rel) == 1) session_free(s);
+}
+
+extern "C" void spissa_session_destroy(spissa_session *s) {
+  if (!s) return;
+  session_release(s);  // freed now, or when its last cache or weight is
 }
 
 namespace {
@@ -302,6 +318,7 @@ static int kv_new_impl(spissa_session *s, size_t num_heads, size_t head_dim, siz
                    hipGetErrorString(e));
   }
   *out = c.release();
+  session_retain(s);
   return SPISSA_OK;
 }
 
@@ -337,7 +354,9 @@ static void kv_release(spissa_kv_cache *c) {
 extern "C" void spissa_kv_cache_free(spissa_kv_cache *c) {
   if (!c) return;
   kv_release(c);
+  spissa_session *s = c->session;
   delete c;
+  session_release(s);
 }
 
 // Converts rows [first, first + n) of the cache into the bf16 shadow, on `st`.
@@ -1195,16 +1214,19 @@ extern "C" int spissa_linear_weight_new(spissa_session *s, int dtype, size_t out
     return set_err(SPISSA_ERR_DEVICE, "weight upload failed: %s", hipGetErrorString(e));
   }
   *out = w.release();
+  session_retain(s);
   return SPISSA_OK;
   GUARD_END
 }
 
 extern "C" void spissa_linear_weight_free(spissa_linear_weight *w) {
   if (!w) return;
-  (void)hipSetDevice(w->session->device);
-  (void)hipStreamSynchronize(w->session->stream);
+  spissa_session *s = w->session;
+  (void)hipSetDevice(s->device);
+  (void)hipStreamSynchronize(s->stream);
   if (w->data) (void)hipFree(w->data);
   delete w;
+  session_release(s);
 }
 
 static int linear_launch(spissa_session *s, const spissa_linear_weight *w, const float *d_x, const float *d_bias,
@@ -1268,6 +1290,99 @@ extern "C" int spissa_linear_device(spissa_session *s, const spissa_linear_weigh
     return set_err(SPISSA_ERR_ARGUMENT, "weight lives on device %d, session on %d", w->session->device, s->device);
   if (batch && (!d_input || !d_out)) return set_err(SPISSA_ERR_ARGUMENT, "null buffer");
   return linear_launch(s, w, d_input, d_bias, batch, d_out);
+  GUARD_END
+}
+
+// ------------------------------------------------------------------------
+// Attention sublayer (models/gemma/generate.rs:178-312,
+// models/llama/generate.rs:200-450)
+// ------------------------------------------------------------------------
+static int check_weight(const spissa_linear_weight *w, size_t out_f, size_t in_f, const char *name,
+                        const spissa_session *s) {
+  if (!w) return set_err(SPISSA_ERR_ARGUMENT, "%s weight is null", name);
+  if (w->out_features != out_f || w->in_features != in_f)
+    return set_err(SPISSA_ERR_SHAPE, "%s weight shape [%zu, %zu] does not match [%zu, %zu]", name, w->out_features,
+                   w->in_features, out_f, in_f);
+  if (w->session->device != s->device) return set_err(SPISSA_ERR_ARGUMENT, "%s weight lives on another device", name);
+  return SPISSA_OK;
+}
+
+extern "C" int spissa_attention_sublayer_device(spissa_session *s, const spissa_attention_layer *L, const float *d_x,
+                                                size_t S, spissa_kv_cache *cache, float *d_out) {
+  GUARD_BEGIN
+  if (!s || !L) return set_err(SPISSA_ERR_ARGUMENT, "null argument");
+  const size_t H = L->hidden, Hq = L->q_heads, Hkv = L->kv_heads, D = L->head_dim;
+  if (!H || !Hq || !Hkv || !D) return set_err(SPISSA_ERR_SHAPE, "sublayer dimensions must be non-zero");
+  if (Hq % Hkv != 0) return set_err(SPISSA_ERR_SHAPE, "query heads %zu must be a multiple of kv heads %zu", Hq, Hkv);
+  ST_TRY(check_weight(L->q_weight, Hq * D, H, "q", s));
+  ST_TRY(check_weight(L->k_weight, Hkv * D, H, "k", s));
+  ST_TRY(check_weight(L->v_weight, Hkv * D, H, "v", s));
+  ST_TRY(check_weight(L->o_weight, H, Hq * D, "o", s));
+  const bool qk_norm = L->d_q_norm != nullptr;
+  if (qk_norm != (L->d_k_norm != nullptr)) return set_err(SPISSA_ERR_ARGUMENT, "q and k norms come together");
+  if (L->rope && (L->rope->kind == SPISSA_ROPE_NEOX || L->rope->rotary_dim != D || L->rope->device != s->device))
+    return set_err(SPISSA_ERR_SHAPE, "the sublayer needs a llama or gemma rope table over the whole head");
+  if (qk_norm && (!L->rope || L->rope->kind != SPISSA_ROPE_GEMMA))
+    return set_err(SPISSA_ERR_ARGUMENT, "the QK-norm prologue needs a gemma rope table");
+  if (!qk_norm && L->q_prescale != 1.0f)
+    return set_err(SPISSA_ERR_ARGUMENT, "a q prescale other than 1 comes with the QK-norm prologue");
+  const size_t pos = cache ? cache->len : 0;
+  if (L->rope && pos + S > L->rope->max_positions)
+    return set_err(SPISSA_ERR_SHAPE, "positions %zu..%zu exceed the rope table (%zu positions)", pos, pos + S,
+                   L->rope->max_positions);
+  if (cache) {
+    if (cache->session != s) return set_err(SPISSA_ERR_ARGUMENT, "the cache belongs to another session");
+    if (cache->num_heads != Hkv || cache->head_dim != D)
+      return set_err(SPISSA_ERR_SHAPE, "cache holds [%zu, %zu] rows, the layer makes [%zu, %zu]", cache->num_heads,
+                     cache->head_dim, Hkv, D);
+    size_t n, nl;  // rotary.rs:227-251: the append must fit before anything runs
+    ST_TRY(kv_validate_append(cache, 0, 0, S, false, &n, &nl));
+  }
+  if (S == 0) return SPISSA_OK;
+  if (!d_x || !d_out) return set_err(SPISSA_ERR_ARGUMENT, "null buffer");
+  spissa_kv_attention_config cfg{S, Hq, Hkv, D, L->causal, L->window};
+  ST_TRY(validate_attention(0, 0, 0, cache, &cfg, false));
+
+  // workspace: normed x, q, k, v, attention output, o projection
+  const size_t sizes[6] = {L->d_input_norm ? S * H : 0, S * Hq * D, S * Hkv * D, S * Hkv * D, S * Hq * D,
+                           L->d_post_norm ? S * H : 0};
+  size_t total = 0;
+  for (size_t n : sizes) total += (n + 63) & ~(size_t)63;
+  ST_TRY(ensure_buf(s, s->sub, std::max<size_t>(total, 64) * sizeof(float), false));
+  float *r[6];
+  {
+    float *p = (float *)s->sub.p;
+    for (int i = 0; i < 6; ++i) {
+      r[i] = p;
+      p += (sizes[i] + 63) & ~(size_t)63;
+    }
+  }
+  HIP_TRY(hipSetDevice(s->device));
+  const float *xn = d_x;
+  if (L->d_input_norm) {
+    HIP_TRY(launch_rms_norm_tree(s->stream, d_x, L->d_input_norm, S, H, L->eps, r[0]));
+    xn = r[0];
+  }
+  float *q = r[1], *k = r[2], *v = r[3], *att = r[4];
+  ST_TRY(linear_launch(s, L->q_weight, xn, nullptr, S, q));
+  ST_TRY(linear_launch(s, L->k_weight, xn, nullptr, S, k));
+  ST_TRY(linear_launch(s, L->v_weight, xn, nullptr, S, v));
+  if (qk_norm)
+    ST_TRY(spissa_gemma_qk_prologue_device(s, L->rope, q, k, S, Hq, Hkv, D, L->d_q_norm, L->d_k_norm, L->eps, pos,
+                                           L->q_prescale));
+  if (S == 1 && cache && decode_supported((int)D, (int)(Hq / Hkv)) && decode_cache_fits(cache)) {
+    // RoPE (Llama), attention and append in the fused decode step
+    spissa_kv_cache *caches[1] = {cache};
+    ST_TRY(spissa_decode_step_device(s, qk_norm ? nullptr : L->rope, q, k, v, caches, 1, &cfg, att));
+  } else {
+    if (!qk_norm && L->rope) ST_TRY(spissa_rope_apply_device(s, L->rope, q, k, S, Hq, Hkv, D, pos));
+    ST_TRY(spissa_attention_device(s, q, k, v, cache, &cfg, att));
+    if (cache) ST_TRY(spissa_kv_cache_append_device(cache, k, v, S));
+  }
+  float *proj = L->d_post_norm ? r[5] : d_out;
+  ST_TRY(linear_launch(s, L->o_weight, att, nullptr, S, proj));
+  if (L->d_post_norm) HIP_TRY(launch_rms_norm_tree(s->stream, proj, L->d_post_norm, S, H, L->eps, d_out));
+  return SPISSA_OK;
   GUARD_END
 }
 

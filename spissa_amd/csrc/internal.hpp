@@ -129,6 +129,10 @@ hipError_t launch_rope_apply(hipStream_t st, const float *cos_tab, const float *
                              size_t kh, size_t D, size_t half);
 hipError_t launch_rms_norm(hipStream_t st, const float *x, const float *w, size_t rows,
                            size_t cols, float eps, float *out);
+// Tree-reduced RMSNorm (not the reference's summation order; rounding-level
+// differences), one workgroup per row: the sublayer's wide norms.
+hipError_t launch_rms_norm_tree(hipStream_t st, const float *x, const float *w, size_t rows, size_t cols,
+                                float eps, float *out);
 hipError_t launch_gemma_prologue(hipStream_t st, const float *cos_tab, const float *sin_tab,
                                  size_t tab_stride, float *q, float *k, size_t S, size_t qh,
                                  size_t kh, size_t D, size_t half, const float *qn,

@@ -48,6 +48,77 @@ __global__ void rms_norm_kernel(const float *__restrict__ x, const float *__rest
   for (int c = 0; c < cols; ++c) o[c] = row[c] * inv_rms * w[c];
 }
 
+// The same sum for wide rows: one workgroup per row stages the row in LDS
+// with coalesced loads, lane 0 of wave 0 adds the squares in index order
+// (bit-identical to the one-thread-per-row kernel), and every thread then
+// scales its share of the row. Rows of up to kNormRowMax floats.
+constexpr int kNormRowMax = 8192;
+__global__ __launch_bounds__(256) void rms_norm_row_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                           int cols, float eps, float *__restrict__ out) {
+#pragma clang fp contract(off)
+  __shared__ float row_s[kNormRowMax];
+  __shared__ float inv_s;
+  const float *row = x + (long)blockIdx.x * cols;
+  for (int c = threadIdx.x; c < cols; c += 256) row_s[c] = row[c];
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float acc = 0.0f;
+    for (int c = 0; c < cols; ++c) acc += row_s[c] * row_s[c];
+    float mean_square = acc / (float)cols;
+    inv_s = 1.0f / sqrtf(mean_square + eps);
+  }
+  __syncthreads();
+  const float inv_rms = inv_s;
+  float *o = out + (long)blockIdx.x * cols;
+  for (int c = threadIdx.x; c < cols; c += 256) o[c] = row_s[c] * inv_rms * w[c];
+}
+
+// RMSNorm with a tree-reduced sum of squares, for the attention sublayer's
+// input and post-attention norms (one workgroup per row): results differ
+// from the sequential sum by rounding only (relative 1e-7), at the cost of a
+// launch instead of a serial chain of `cols` additions.
+__global__ __launch_bounds__(256) void rms_norm_tree_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                            int cols, float eps, float *__restrict__ out) {
+  __shared__ float part[4];
+  const float *row = x + (long)blockIdx.x * cols;
+  float *o = out + (long)blockIdx.x * cols;
+  // 16-byte pieces when the rows allow it, four loads in flight per thread
+  const bool vec = (cols & 3) == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
+                                        reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+  float acc = 0.0f;
+  if (vec) {
+    const float4 *r4 = reinterpret_cast<const float4 *>(row);
+#pragma unroll 4
+    for (int c = threadIdx.x; c < (cols >> 2); c += 256) {
+      const float4 v = r4[c];
+      acc = fmaf(v.x, v.x, acc);
+      acc = fmaf(v.y, v.y, acc);
+      acc = fmaf(v.z, v.z, acc);
+      acc = fmaf(v.w, v.w, acc);
+    }
+  } else {
+#pragma unroll 4
+    for (int c = threadIdx.x; c < cols; c += 256) acc = fmaf(row[c], row[c], acc);
+  }
+  for (int d = 32; d > 0; d >>= 1) acc += __shfl_xor(acc, d, 64);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  const float total = (part[0] + part[1]) + (part[2] + part[3]);
+  const float inv_rms = 1.0f / sqrtf(total / (float)cols + eps);
+  if (vec) {
+    const float4 *r4 = reinterpret_cast<const float4 *>(row);
+    const float4 *w4 = reinterpret_cast<const float4 *>(w);
+    float4 *o4 = reinterpret_cast<float4 *>(o);
+#pragma unroll 4
+    for (int c = threadIdx.x; c < (cols >> 2); c += 256) {
+      const float4 v = r4[c], g = w4[c];
+      o4[c] = make_float4(v.x * inv_rms * g.x, v.y * inv_rms * g.y, v.z * inv_rms * g.z, v.w * inv_rms * g.w);
+    }
+  } else {
+    for (int c = threadIdx.x; c < cols; c += 256) o[c] = row[c] * inv_rms * w[c];
+  }
+}
+
 // models/gemma/generate.rs:230-278 for one row of q or k: rms_norm, Gemma
 // rotate-half with the layer's table, then (q rows only) the prescale.
 __global__ void gemma_prologue_kernel(const float *__restrict__ cos_tab,
@@ -171,8 +242,19 @@ hipError_t launch_rope_apply(hipStream_t st, const float *cos_tab, const float *
 hipError_t launch_rms_norm(hipStream_t st, const float *x, const float *w, size_t rows,
                            size_t cols, float eps, float *out) {
   if (rows == 0) return hipSuccess;
-  hipLaunchKernelGGL(rms_norm_kernel, dim3(blocks_for((long)rows, 64)), dim3(64), 0, st, x, w,
-                     (long)rows, (int)cols, eps, out);
+  // wide rows: a workgroup per row, so loads are coalesced and never serial
+  if (cols >= 512 && cols <= (size_t)kNormRowMax)
+    hipLaunchKernelGGL(rms_norm_row_kernel, dim3((unsigned)rows), dim3(256), 0, st, x, w, (int)cols, eps, out);
+  else
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(blocks_for((long)rows, 64)), dim3(64), 0, st, x, w,
+                       (long)rows, (int)cols, eps, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_rms_norm_tree(hipStream_t st, const float *x, const float *w, size_t rows, size_t cols,
+                                float eps, float *out) {
+  if (rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(rms_norm_tree_kernel, dim3((unsigned)rows), dim3(256), 0, st, x, w, (int)cols, eps, out);
   return hipGetLastError();
 }
 

@@ -9,6 +9,7 @@ rotary.rs:560-564 does).
 from __future__ import annotations
 
 import ctypes as C
+from dataclasses import dataclass
 from typing import Optional, Sequence
 
 from . import _ffi
@@ -64,6 +65,43 @@ class RopeTable:
             self.close()
         except Exception:
             pass
+
+
+@dataclass
+class AttentionLayer:
+    """One layer's attention sublayer (spissa_attention_layer): the four
+    projection weights (spissa_amd.linear.LinearWeight on this session's
+    device), the norm multipliers as device tensors (None: that norm is
+    absent), the layer's rope table (None: no RoPE), and the attention
+    parameters. Mirrors the arguments models/gemma/generate.rs:178-312 and
+    models/llama/generate.rs:200-450 take from the model build."""
+
+    hidden: int
+    q_heads: int
+    kv_heads: int
+    head_dim: int
+    q_weight: object
+    k_weight: object
+    v_weight: object
+    o_weight: object
+    input_norm: object = None
+    q_norm: object = None
+    k_norm: object = None
+    post_norm: object = None
+    eps: float = 1e-6
+    rope: Optional[RopeTable] = None
+    q_prescale: float = 1.0
+    causal: bool = True
+    window: int = 0
+
+    def _c(self) -> _ffi.AttentionLayerC:
+        return _ffi.AttentionLayerC(
+            self.hidden, self.q_heads, self.kv_heads, self.head_dim, self.q_weight.handle.value,
+            self.k_weight.handle.value, self.v_weight.handle.value, self.o_weight.handle.value,
+            _dev(self.input_norm, "input_norm") or None, _dev(self.q_norm, "q_norm") or None,
+            _dev(self.k_norm, "k_norm") or None, _dev(self.post_norm, "post_norm") or None, self.eps,
+            None if self.rope is None else self.rope.handle.value, self.q_prescale, 1 if self.causal else 0,
+            self.window)
 
 
 class Session:
@@ -164,6 +202,14 @@ class Session:
 
     def append(self, cache: KvCache, k, v, token_count: int) -> None:
         cache.append_device(_dev(k, "k"), _dev(v, "v"), token_count)
+
+    def attention_sublayer(self, layer: AttentionLayer, x, seq_len: int, cache: Optional[KvCache], out) -> None:
+        """x [seq_len, hidden] -> out [seq_len, hidden]: norm, projections, QK-norm, RoPE at the
+        cache's next positions, attention, append, o projection, post norm."""
+        lc = layer._c()
+        check(self._lib.spissa_attention_sublayer_device(
+            self.handle, C.byref(lc), _dev(x, "x"), seq_len, None if cache is None else cache.handle,
+            _dev(out, "out")))
 
     def linear_weight(self, data, dtype: int, out_features: int, in_features: int):
         """A weight resident on this session's device (see spissa_amd.linear.LinearWeight)."""

@@ -84,8 +84,10 @@ def test_resident_rope_table_matches_drop_in(gpu):
         s.rope_apply(t, dq, dk, S, Hq, Hkv, D, 8192 + 64 - S + 1)
 
 
-def test_rms_norm_bitwise(gpu):
-    rows, cols = 4096 * 8, 256
+@pytest.mark.parametrize("rows,cols", [(4096 * 8, 256), (1, 3072), (16, 1152), (7, 2560), (3, 8192), (2, 9000)])
+def test_rms_norm_bitwise(gpu, rows, cols):
+    # head rows (one thread per row), model-width rows (a workgroup per row), and
+    # rows beyond the staged width (one thread per row again)
     x, w = normal_f32(99, rows * cols), normal_f32(100, cols, 1.0, 0.1)
     assert_bitwise(gpu.rms_norm(x, w, rows, cols, 1e-6), o.rms_norm(x, w, rows, cols, 1e-6), "rms_norm")
 
