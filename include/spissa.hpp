@@ -413,6 +413,31 @@ class RopeTable {
   spissa_rope_table *t_ = nullptr;
 };
 
+// One layer's attention sublayer (models/gemma/generate.rs:178-312,
+// models/llama/generate.rs:200-450): weights, norm multipliers (device
+// pointers, nullptr: that norm is absent), the layer's rope table.
+struct AttentionLayer {
+  size_t hidden, q_heads, kv_heads, head_dim;
+  const LinearWeight *q_weight, *k_weight, *v_weight, *o_weight;
+  const float *d_input_norm = nullptr;
+  const float *d_q_norm = nullptr;
+  const float *d_k_norm = nullptr;
+  const float *d_post_norm = nullptr;
+  float eps = 1e-6f;
+  const RopeTable *rope = nullptr;
+  float q_prescale = 1.0f;
+  bool causal = true;
+  size_t window = 0;
+
+  spissa_attention_layer c() const {
+    return spissa_attention_layer{hidden, q_heads, kv_heads, head_dim, q_weight ? q_weight->raw() : nullptr,
+                                  k_weight ? k_weight->raw() : nullptr, v_weight ? v_weight->raw() : nullptr,
+                                  o_weight ? o_weight->raw() : nullptr, d_input_norm, d_q_norm, d_k_norm,
+                                  d_post_norm, eps, rope ? rope->raw() : nullptr, q_prescale, causal ? 1 : 0,
+                                  window};
+  }
+};
+
 // One device and one HIP stream. Calls are asynchronous on that stream;
 // sync() waits and reports device-side errors.
 class Session {
@@ -498,6 +523,14 @@ class Session {
     const auto c = cfg.c();
     return detail::check(
         spissa_attention_decode_batch_device(s_, d_q, d_k, d_v, raw.data(), raw.size(), &c, d_out));
+  }
+  // The attention sublayer of one layer: d_x [seq_len, hidden] -> d_out; RoPE
+  // positions continue the cache, whose rows receive the rotated k and v.
+  Result<void> attention_sublayer(const AttentionLayer &layer, const float *d_x, size_t seq_len, KvCache *cache,
+                                  float *d_out) const {
+    const auto c = layer.c();
+    return detail::check(
+        spissa_attention_sublayer_device(s_, &c, d_x, seq_len, cache ? cache->raw() : nullptr, d_out));
   }
   // out[batch, out] = x[batch, in] x W^T + bias on device buffers (d_bias may be null).
   Result<void> linear(const LinearWeight &w, const float *d_x, const float *d_bias, size_t batch,

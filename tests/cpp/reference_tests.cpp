@@ -438,6 +438,78 @@ TEST(linear_rejects_mismatched_shapes_and_bytes) {
   CHECK(bad_bytes.is_err() && bad_bytes.error().kind == ErrorKind::InvalidTensorData);
 }
 
+// models/llama/generate.rs:200-450 on the device in one call equals the same
+// sequence through the drop-in API: rms_norm, three projections, RoPE at the
+// cache's next position, cached attention, append, o projection.
+TEST(attention_sublayer_matches_the_dropin_sequence) {
+  const size_t H = 256, Hq = 4, Hkv = 2, D = 64, P = 9;
+  const float base = 500000.0f, eps = 1e-5f;
+  uint32_t st = 7u;
+  auto draw = [&](size_t n, float scale) {
+    std::vector<float> v(n);
+    for (auto &e : v) {
+      st = st * 1664525u + 1013904223u;
+      e = scale * ((float)((st >> 8) & 0xffff) / 32768.0f - 1.0f);
+    }
+    return v;
+  };
+  auto x = draw(H, 1.0f), norm = draw(H, 0.1f), wq = draw(Hq * D * H, 0.05f), wk = draw(Hkv * D * H, 0.05f),
+       wv = draw(Hkv * D * H, 0.05f), wo = draw(H * Hq * D, 0.05f), pk = draw(P * Hkv * D, 1.0f),
+       pv = draw(P * Hkv * D, 1.0f);
+  for (auto &g : norm) g += 1.0f;
+
+  // drop-in sequence on the default session
+  auto Wq = ok(LinearWeight::create(DType::F32, Hq * D, H, wq.data(), wq.size() * 4));
+  auto Wk = ok(LinearWeight::create(DType::F32, Hkv * D, H, wk.data(), wk.size() * 4));
+  auto Wv = ok(LinearWeight::create(DType::F32, Hkv * D, H, wv.data(), wv.size() * 4));
+  auto Wo = ok(LinearWeight::create(DType::F32, H, Hq * D, wo.data(), wo.size() * 4));
+  auto ref_cache = ok(KvCache::create(Hkv, D, P + 1));
+  ok(ref_cache.append(pk, pv, P));
+  auto xn = ok(ops::rms_norm(x, norm, 1, H, eps));
+  auto q = ok(linear(Wq, xn, nullptr, StreamingLinearConfig{1, H, Hq * D}));
+  auto k = ok(linear(Wk, xn, nullptr, StreamingLinearConfig{1, H, Hkv * D}));
+  auto v = ok(linear(Wv, xn, nullptr, StreamingLinearConfig{1, H, Hkv * D}));
+  ok(apply_llama_rotary_inplace(q, k, Hq, Hkv, RotaryEmbeddingConfig{1, Hq, D, D, base, P}));
+  auto att = ok(scaled_dot_product_attention_with_cache(q, k, v, &ref_cache, KvAttentionConfig{1, Hq, Hkv, D, true}));
+  ok(ref_cache.append(k, v, 1));
+  auto expected = ok(linear(Wo, att, nullptr, StreamingLinearConfig{1, Hq * D, H}));
+
+  // one device call
+  auto session = ok(Session::create(0));
+  auto sq = ok(session.linear_weight(DType::F32, Hq * D, H, wq.data(), wq.size() * 4));
+  auto sk = ok(session.linear_weight(DType::F32, Hkv * D, H, wk.data(), wk.size() * 4));
+  auto sv = ok(session.linear_weight(DType::F32, Hkv * D, H, wv.data(), wv.size() * 4));
+  auto so = ok(session.linear_weight(DType::F32, H, Hq * D, wo.data(), wo.size() * 4));
+  auto cache = ok(session.kv_cache(Hkv, D, P + 1));
+  ok(cache.append(pk, pv, P));
+  auto table = ok(session.rope_table(RopeKind::Llama, D, base, P + 1));
+  float *dx = nullptr, *dnorm = nullptr, *dout = nullptr;
+  CHECK(hipMalloc(&dx, H * 4) == hipSuccess && hipMalloc(&dnorm, H * 4) == hipSuccess &&
+        hipMalloc(&dout, H * 4) == hipSuccess);
+  CHECK(hipMemcpy(dx, x.data(), H * 4, hipMemcpyHostToDevice) == hipSuccess);
+  CHECK(hipMemcpy(dnorm, norm.data(), H * 4, hipMemcpyHostToDevice) == hipSuccess);
+  AttentionLayer layer{H, Hq, Hkv, D, &sq, &sk, &sv, &so};
+  layer.d_input_norm = dnorm;
+  layer.eps = eps;
+  layer.rope = &table;
+  ok(session.attention_sublayer(layer, dx, 1, &cache, dout));
+  ok(session.sync());
+  std::vector<float> got(H);
+  CHECK(hipMemcpy(got.data(), dout, H * 4, hipMemcpyDeviceToHost) == hipSuccess);
+  (void)hipFree(dx);
+  (void)hipFree(dnorm);
+  (void)hipFree(dout);
+
+  float ref_max = 0.0f;
+  for (float e : expected) ref_max = std::fmax(ref_max, std::fabs(e));
+  assert_close_vec(got, expected, 1e-5f * ref_max);
+  CHECK(cache.len() == P + 1);
+  const auto ck = cache.keys(), rk = ref_cache.keys();
+  float kmax = 0.0f;
+  for (float e : rk) kmax = std::fmax(kmax, std::fabs(e));
+  assert_close_vec(ck, rk, 1e-5f * kmax);
+}
+
 // --------------------------------------------------- ABI contract (no Rust test)
 
 // rotary.rs:17-38: round down to an even count; errors for empty results.
