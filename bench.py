@@ -286,6 +286,8 @@ def gpu_bench(args) -> dict:
         if not args.decode_only:
             log("timing projections")
             res["projections"] = projection_bench(sess, stream, gen, dev, args, time_graph)
+            log("timing the LM head")
+            res["lm_head"] = lm_head_bench(sess, stream, gen, dev, args, time_graph)
     return res
 
 
@@ -384,6 +386,60 @@ def projection_bench(sess, stream, gen, dev, args, time_graph) -> dict:
     return out
 
 
+# Tied LM heads (vocab, hidden) timed by lm_head_bench.
+LM_HEADS = {"llama32_3b": (128256, 3072), "gemma3_1b": (262144, 1152)}
+
+
+def lm_head_bench(sess, stream, gen, dev, args, time_graph) -> dict:
+    """The greedy decode tail: logits = table x hidden over the bf16 tied
+    embedding, then the argmax token, per generated token. Two copies of each
+    table alternate so that no replay finds the previous one in the 256 MB
+    last-level cache."""
+    import torch
+
+    from spissa_amd.linear import DTYPE_BF16
+
+    out = {}
+    for name, (vocab, hid) in LM_HEADS.items():
+        with torch.cuda.stream(stream):
+            bits = (torch.randn(vocab * hid, generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+            tables = [sess.linear_weight(bits, DTYPE_BF16, vocab, hid) for _ in range(2)]
+        del bits
+        with torch.cuda.stream(stream):
+            x = torch.randn(hid, generator=gen, device=dev)
+            logits = torch.empty(vocab, device=dev)
+            tok = torch.zeros(1, dtype=torch.int32, device=dev)
+        reps = 8
+        rec = {}
+        for part in ("token", "logits", "argmax"):
+            def step():
+                for r in range(reps):
+                    if part == "argmax":
+                        sess.argmax(logits, vocab, tok)
+                    else:
+                        sess.lm_head(tables[r % 2], x, logits, tok if part == "token" else None)
+
+            step()
+            sess.sync()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                step()
+            rec[f"{part}_us"] = round(time_graph(g, max(3, args.steps // 2), 2) * 1e3 / reps, 3)
+            del g
+        tbytes = vocab * hid * 2
+        # table + hidden read, logits written by the GEMV and read by the argmax
+        step_bytes = tbytes + hid * 4 + 2 * vocab * 4
+        rec["GBps"] = round(step_bytes / (rec["token_us"] * 1e-6) / 1e9, 1)
+        rec["hbm_frac"] = round(rec["GBps"] / HBM_PEAK_GBS, 4)
+        rec["logits_GBps"] = round((tbytes + hid * 4 + vocab * 4) / (rec["logits_us"] * 1e-6) / 1e9, 1)
+        rec["tokens_per_s"] = round(1e6 / rec["token_us"], 1)
+        rec["table_bytes"] = tbytes
+        out[name] = rec
+        del tables, x, logits, tok
+        torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(args) -> dict:
     """The oracle (C restatement of the reference) on this host, bounded sample."""
     import numpy as np
@@ -456,6 +512,23 @@ def cpu_baseline(args) -> dict:
         out["projection_b1"] = {
             "value": qkv * hid * 2 / tl / 1e9, "unit": "GB/s of weights", "us_per_layer": tl * 1e6, "cores": 1,
             "sample": "oracle linear, Llama-3.2-3B fused q/k/v weight (5120 x 3072 bf16), batch 1, median of 3"}
+        # The LM head over the Llama-3.2-3B tied table (128256 x 3072 bf16) and the
+        # argmax (the reference's serial lm_head_logits_rows_bf16 + sample_argmax).
+        vocab, hid = LM_HEADS["llama32_3b"]
+        import torch
+
+        g = torch.Generator(device="cuda").manual_seed(13)  # synthetic data only: drawn on the device
+        tb = (torch.randn(vocab * hid, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+        tbits = tb.view(torch.int16).cpu().numpy().view(np.uint16)
+        del tb
+        x = normal_f32(seed_for(3, 0, 3, "q"), hid)
+        t0 = time.perf_counter()
+        lg = oracle.lm_head_logits(x, tbits, oracle.DTYPE_BF16, vocab, hid)
+        oracle.sample_argmax(lg)
+        th = time.perf_counter() - t0
+        out["lm_head_b1"] = {
+            "value": vocab * hid * 2 / th / 1e9, "unit": "GB/s of table", "us_per_token": th * 1e6, "cores": 1,
+            "sample": "oracle LM head + argmax, Llama-3.2-3B tied table (128256 x 3072 bf16), one token"}
     return out
 
 
@@ -529,6 +602,11 @@ def main() -> int:
         line["projections"] = {"workload": "llama-3.2-3B fused q/k/v projection, 5120 x 3072 bf16 weight "
                                            "resident in HBM, f32 activations and output",
                                **res["projections"]}
+    if "lm_head" in res:
+        line["lm_head"] = {"workload": "greedy decode tail per token: tied-embedding LM head over the bf16 "
+                                       "table (logits GEMV) + argmax token; token_us = both, logits_us = GEMV "
+                                       "only, argmax_us = argmax only",
+                           **res["lm_head"]}
     if cpu is not None:
         line["cpu_baseline"] = cpu
     print(json.dumps(line), flush=True)

@@ -1,7 +1,8 @@
 // spissa.hpp -- C++17 mirror of the Spissa runtime's attention API
 // (crates/spissa-runtime/src/rotary.rs, ops.rs, models/gemma/model.rs) and of
-// the streaming linear projections either side of it (streaming/linear.rs)
-// over the C ABI of spissa_hip.h. Header-only; link with libspissa_hip.so.
+// the streaming linear projections either side of it (streaming/linear.rs),
+// the LM head and greedy sampling (streaming/mod.rs, ops.rs) over the C ABI
+// of spissa_hip.h. Header-only; link with libspissa_hip.so.
 //
 // The names, argument order and meaning follow the Rust functions they
 // replace, so code (and tests) written against the reference read the same:
@@ -12,6 +13,7 @@
 //   KvCache::new(h, d, max)                    spissa::KvCache::create(h, d, max)
 //   Option<&KvCache>                           const spissa::KvCache* (nullptr = None)
 //   Option<&[f32]>                             const std::vector<float>* (nullptr = None)
+//   Option<usize>                              std::optional<size_t>
 //   LazySpissaModel + weight name              spissa::LinearModel (resident weights by name)
 // Errors are returned, never thrown; Result<T>::unwrap() throws
 // std::runtime_error for callers that prefer exceptions (as .unwrap() panics).
@@ -21,7 +23,9 @@
 #pragma once
 
 #include <cstddef>
+#include <cstdint>
 #include <map>
+#include <optional>
 #include <stdexcept>
 #include <string>
 #include <type_traits>
@@ -321,11 +325,17 @@ class LinearWeight {
   static Result<LinearWeight> create(DType dtype, size_t out_features, size_t in_features, const void *data,
                                      size_t data_bytes, const Session *session = nullptr);
   LinearWeight() = default;
-  LinearWeight(LinearWeight &&o) noexcept : w_(o.w_) { o.w_ = nullptr; }
+  LinearWeight(LinearWeight &&o) noexcept
+      : w_(o.w_), dtype_(o.dtype_), out_features_(o.out_features_), in_features_(o.in_features_) {
+    o.w_ = nullptr;
+  }
   LinearWeight &operator=(LinearWeight &&o) noexcept {
     if (this != &o) {
       if (w_) spissa_linear_weight_free(w_);
       w_ = o.w_;
+      dtype_ = o.dtype_;
+      out_features_ = o.out_features_;
+      in_features_ = o.in_features_;
       o.w_ = nullptr;
     }
     return *this;
@@ -336,10 +346,16 @@ class LinearWeight {
     if (w_) spissa_linear_weight_free(w_);
   }
   spissa_linear_weight *raw() const { return w_; }
+  DType dtype() const { return dtype_; }
+  size_t out_features() const { return out_features_; }
+  size_t in_features() const { return in_features_; }
 
  private:
-  explicit LinearWeight(spissa_linear_weight *w) : w_(w) {}
+  LinearWeight(spissa_linear_weight *w, DType dtype, size_t out_features, size_t in_features)
+      : w_(w), dtype_(dtype), out_features_(out_features), in_features_(in_features) {}
   spissa_linear_weight *w_ = nullptr;
+  DType dtype_ = DType::F32;
+  size_t out_features_ = 0, in_features_ = 0;
 };
 
 // Resident weights by tensor name: the role of lazy.rs's LazySpissaModel.
@@ -381,6 +397,53 @@ inline Result<std::vector<float>> streaming_tile_linear_from_model(const LinearM
   if (w.is_err()) return w.error();
   return linear(*w.value(), input, bias, config.linear);
 }
+
+// ---- LM head and greedy sampling (streaming/mod.rs:186-287, ops.rs:309-348) ----
+
+namespace detail {
+inline Result<std::vector<float>> lm_head(Slice<const float> last_hidden, const LinearWeight &table,
+                                          size_t vocab_size, size_t hidden, DType want) {
+  if (table.dtype() != want)
+    return RuntimeError{ErrorKind::InvalidTensorData, "LM head table dtype does not match this variant"};
+  if (table.out_features() != vocab_size || table.in_features() != hidden)
+    return RuntimeError{ErrorKind::Shape, "LM head table shape does not match vocab_size x hidden"};
+  std::vector<float> logits(vocab_size);
+  auto r = detail::check(spissa_lm_head_logits(table.raw(), last_hidden.ptr, last_hidden.len, logits.data(),
+                                               logits.size()));
+  if (r.is_err()) return r.error();
+  return logits;
+}
+inline int64_t excluded_arg(std::optional<size_t> e) {
+  // an index past INT64_MAX is past any logits buffer: plain sample_argmax either way
+  return e && *e <= static_cast<size_t>(INT64_MAX) ? static_cast<int64_t>(*e) : -1;
+}
+}  // namespace detail
+
+// streaming/mod.rs:186-221: logits[v] = sum_h last_hidden[h] * table[v, h] over a
+// resident f32 table [vocab_size, hidden] (the tied embedding).
+inline Result<std::vector<float>> lm_head_logits_parallel(Slice<const float> last_hidden, const LinearWeight &table,
+                                                          size_t vocab_size, size_t hidden) {
+  return detail::lm_head(last_hidden, table, vocab_size, hidden, DType::F32);
+}
+// streaming/mod.rs:238-272, resident bf16 table.
+inline Result<std::vector<float>> lm_head_logits_parallel_bf16(Slice<const float> last_hidden,
+                                                               const LinearWeight &table, size_t vocab_size,
+                                                               size_t hidden) {
+  return detail::lm_head(last_hidden, table, vocab_size, hidden, DType::Bf16);
+}
+
+// ops.rs:326-348 (std::nullopt: ops.rs:309-324 sample_argmax), on the calling
+// thread's default session.
+inline Result<size_t> sample_argmax_excluding(Slice<const float> logits, std::optional<size_t> excluded_token) {
+  spissa_session *s = nullptr;
+  auto r = detail::check(spissa_default_session(&s));
+  if (r.is_err()) return r.error();
+  size_t token = 0;
+  r = detail::check(spissa_sample_argmax(s, logits.ptr, logits.len, detail::excluded_arg(excluded_token), &token));
+  if (r.is_err()) return r.error();
+  return token;
+}
+inline Result<size_t> sample_argmax(Slice<const float> logits) { return sample_argmax_excluding(logits, std::nullopt); }
 
 // ---- device tier (no reference counterpart): device pointers, one stream ----
 
@@ -541,6 +604,17 @@ class Session {
                                      size_t data_bytes) const {
     return LinearWeight::create(dtype, out_features, in_features, data, data_bytes, this);
   }
+  // d_token[0] = sample_argmax_excluding(d_logits[0..n), excluded) on the device.
+  Result<void> argmax(const float *d_logits, size_t n, int32_t *d_token,
+                      std::optional<size_t> excluded = std::nullopt) const {
+    return detail::check(spissa_argmax_device(s_, d_logits, n, detail::excluded_arg(excluded), d_token));
+  }
+  // The greedy decode tail: d_logits = table x d_hidden, then (d_token set) its argmax.
+  Result<void> lm_head(const LinearWeight &table, const float *d_hidden, float *d_logits, int32_t *d_token = nullptr,
+                       std::optional<size_t> excluded = std::nullopt) const {
+    return detail::check(
+        spissa_lm_head_device(s_, table.raw(), d_hidden, detail::excluded_arg(excluded), d_logits, d_token));
+  }
   // RoPE + attention + append of one decode step of one layer (table = nullptr: no RoPE).
   Result<void> decode_step(const RopeTable *table, const float *d_q, const float *d_k, const float *d_v,
                            const std::vector<KvCache *> &caches, const KvAttentionConfig &cfg, float *d_out) const {
@@ -569,7 +643,7 @@ inline Result<LinearWeight> LinearWeight::create(DType dtype, size_t out_feature
   auto r = detail::check(
       spissa_linear_weight_new(s, static_cast<int>(dtype), out_features, in_features, data, data_bytes, &w));
   if (r.is_err()) return r.error();
-  return LinearWeight(w);
+  return LinearWeight(w, dtype, out_features, in_features);
 }
 
 }  // namespace spissa

@@ -1,7 +1,8 @@
 /*
  * spissa_hip.h -- C ABI of the MI355X (gfx950) attention path for the Spissa
  * runtime: RoPE, the per-layer KV cache, cached SDPA (decode and causal GQA
- * prefill), the Gemma 3 QK-norm, and the linear projections either side.
+ * prefill), the Gemma 3 QK-norm, the linear projections either side, and
+ * the LM head with greedy sampling after the last layer.
  *
  * Every symbol here replaces one Rust item of crates/spissa-runtime; the
  * citation next to each declaration names it (paths relative to the
@@ -242,7 +243,9 @@ typedef struct spissa_linear_weight spissa_linear_weight;
 /* Uploads a row-major [out_features, in_features] weight whose little-endian
  * element bytes are `data` (what a raw chunk of the container holds).
  * data_bytes must equal out_features * in_features * element size
- * (streaming/validation.rs:258-289: InvalidTensorData otherwise). */
+ * (streaming/validation.rs:258-289: InvalidTensorData otherwise). `data` may
+ * be host memory or device memory of any device; work that produces it on
+ * another stream must be complete before the call. */
 int spissa_linear_weight_new(spissa_session *s, int dtype, size_t out_features, size_t in_features,
                              const void *data, size_t data_bytes, spissa_linear_weight **out);
 /* Frees the weight after the work queued on its session. */
@@ -264,6 +267,35 @@ int spissa_linear(const spissa_linear_weight *w, const float *input, size_t inpu
  * d_out [batch, out]), asynchronous on the session stream. */
 int spissa_linear_device(spissa_session *s, const spissa_linear_weight *w, const float *d_input,
                          const float *d_bias, size_t batch, float *d_out);
+
+/* ------------------------------------------------------------------------ */
+/* LM head and greedy sampling: the tied embedding table as the output      */
+/* projection of the last hidden row, then the argmax over the vocabulary.  */
+/* ------------------------------------------------------------------------ */
+
+/* streaming/mod.rs:186-236 lm_head_logits_parallel (f32 table) and
+ * streaming/mod.rs:238-287 lm_head_logits_parallel_bf16 (bf16 table):
+ * logits[v] = sum_h last_hidden[h] * table[v, h], with the table a
+ * [vocab_size, hidden] spissa_linear_weight of dtype F32 or BF16 (other
+ * dtypes: InvalidTensorData). last_hidden_len must equal hidden and
+ * logits_len vocab_size (Shape otherwise; the reference indexes past such
+ * buffers instead). Host buffers, synchronous. */
+int spissa_lm_head_logits(const spissa_linear_weight *table, const float *last_hidden,
+                          size_t last_hidden_len, float *logits, size_t logits_len);
+/* ops.rs:309-324 sample_argmax (excluded < 0: Option::None) and
+ * ops.rs:326-348 sample_argmax_excluding (excluded >= 0: Some(excluded)) over
+ * host logits, on the session's device: the first maximal index, with the
+ * reference's NaN and tie behaviour. n == 0: InvalidTensorData
+ * ("cannot sample from empty logits"). n <= INT32_MAX - 1024 (Shape). */
+int spissa_sample_argmax(spissa_session *s, const float *logits, size_t n, int64_t excluded,
+                         size_t *token);
+/* Same over device logits; the index is written to d_token[0] (int32). */
+int spissa_argmax_device(spissa_session *s, const float *d_logits, size_t n, int64_t excluded,
+                         int32_t *d_token);
+/* The greedy decode tail on the device: d_logits [vocab] = table x d_hidden
+ * [hidden], then, unless d_token is NULL, d_token[0] = the argmax as above. */
+int spissa_lm_head_device(spissa_session *s, const spissa_linear_weight *table, const float *d_hidden,
+                          int64_t excluded, float *d_logits, int32_t *d_token);
 
 /* ------------------------------------------------------------------------ */
 /* The attention sublayer of one layer on the device, in the reference's    */

@@ -89,6 +89,9 @@ def load() -> C.CDLL:
         "or_fp16_to_f32": (C.c_float, [C.c_uint16]),
         "or_f32_to_bf16_rne": (C.c_uint16, [C.c_float]),
         "or_linear": (C.c_int, [_fp, _sz, C.c_void_p, C.c_int, _sz, _fp, _sz, _sz, _sz, _sz, _fp]),
+        "or_lm_head_logits": (C.c_int, [_fp, _sz, C.c_void_p, C.c_int, _sz, _sz, _fp]),
+        "or_sample_argmax": (C.c_int, [_fp, _sz, C.POINTER(_sz)]),
+        "or_sample_argmax_excluding": (C.c_int, [_fp, _sz, C.c_int, _sz, C.POINTER(_sz)]),
         "or_sdpa_many_threads": (C.c_int, [_sz, C.POINTER(_fp), C.POINTER(_fp), C.POINTER(_fp),
                                            C.POINTER(C.POINTER(KvC)), C.POINTER(AttnCfg),
                                            C.POINTER(_fp), C.c_int]),
@@ -260,4 +263,32 @@ def linear(x, w, dtype, bias, batch, in_features, out_features) -> np.ndarray:
     _check(load().or_linear(_p(x), x.size, w.ctypes.data_as(C.c_void_p), dtype, w.size, _p(bias),
                             0 if bias is None else bias.size, batch, in_features, out_features, _p(out)))
     return out
+
+
+def lm_head_logits(last_hidden, table, dtype, vocab_size, hidden) -> np.ndarray:
+    """streaming/mod.rs:186-287 (serial row loop). table: float32 (DTYPE_F32)
+    or uint16 bf16 bits (DTYPE_BF16), [vocab_size, hidden] row-major."""
+    want = np.float32 if dtype == DTYPE_F32 else np.uint16
+    assert table.dtype == want and table.flags.c_contiguous and table.size == vocab_size * hidden
+    out = np.empty(vocab_size, dtype=np.float32)
+    _check(load().or_lm_head_logits(_p(last_hidden), last_hidden.size, table.ctypes.data_as(C.c_void_p),
+                                    dtype, vocab_size, hidden, _p(out)))
+    return out
+
+
+def sample_argmax(logits) -> int:
+    """ops.rs:309-324"""
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    r = _sz(0)
+    _check(load().or_sample_argmax(_p(x), x.size, C.byref(r)))
+    return r.value
+
+
+def sample_argmax_excluding(logits, excluded: Optional[int]) -> int:
+    """ops.rs:326-348"""
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    r = _sz(0)
+    _check(load().or_sample_argmax_excluding(_p(x), x.size, 0 if excluded is None else 1,
+                                             0 if excluded is None else excluded, C.byref(r)))
+    return r.value
 

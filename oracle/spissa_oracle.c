@@ -628,3 +628,50 @@ int or_linear(const float *input, size_t input_len, const void *weight, int dtyp
     return OR_OK;
 }
 
+int or_lm_head_logits(const float *last_hidden, size_t hidden_len, const void *table, int dtype,
+                      size_t vocab_size, size_t hidden, float *logits) {
+    if (dtype != OR_DTYPE_F32 && dtype != OR_DTYPE_BF16)
+        return fail(OR_INVALID, "LM head table must be f32 or bf16 (dtype %d)", dtype);
+    if (hidden_len != hidden) return fail(OR_SHAPE, "last_hidden holds %zu floats, hidden is %zu", hidden_len, hidden);
+    for (size_t v = 0; v < vocab_size; ++v) {
+        float sum = 0.0f;
+        const size_t row = v * hidden;
+        for (size_t h = 0; h < hidden; ++h) sum += last_hidden[h] * weight_at(table, dtype, row + h);
+        logits[v] = sum;
+    }
+    return OR_OK;
+}
+
+int or_sample_argmax(const float *logits, size_t n, size_t *out) {
+    if (n == 0) return fail(OR_INVALID, "cannot sample from empty logits");
+    size_t best_index = 0;
+    float best_value = logits[0];
+    for (size_t i = 1; i < n; ++i) {
+        if (logits[i] > best_value) {
+            best_index = i;
+            best_value = logits[i];
+        }
+    }
+    *out = best_index;
+    return OR_OK;
+}
+
+int or_sample_argmax_excluding(const float *logits, size_t n, int has_excluded, size_t excluded,
+                               size_t *out) {
+    if (!has_excluded || excluded >= n || n <= 1) return or_sample_argmax(logits, n, out);
+    int have = 0;
+    size_t best_index = 0;
+    float best_value = 0.0f;
+    for (size_t i = 0; i < n; ++i) {
+        if (i == excluded) continue;
+        /* ops.rs:339-342: keep the best only while value <= best */
+        if (have && logits[i] <= best_value) continue;
+        have = 1;
+        best_index = i;
+        best_value = logits[i];
+    }
+    if (!have) return fail(OR_INVALID, "cannot sample from empty logits");
+    *out = best_index;
+    return OR_OK;
+}
+

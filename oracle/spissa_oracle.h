@@ -117,6 +117,19 @@ uint16_t or_f32_to_bf16_rne(float x);
 int or_linear(const float *input, size_t input_len, const void *weight, int dtype, size_t weight_elems,
               const float *bias, size_t bias_len, size_t batch, size_t in_features,
               size_t out_features, float *out);
+/* streaming/mod.rs:223-236 lm_head_logits_rows (f32 table, dtype OR_DTYPE_F32)
+ * and streaming/mod.rs:274-287 with the scalar row dot of streaming/mod.rs:309-319
+ * (bf16 table, OR_DTYPE_BF16): logits[v] = sum_h last_hidden[h] * table[v][h],
+ * from 0.0 in index order with each product rounded. The parallel entry
+ * points (streaming/mod.rs:186-221, 238-272) only split the rows over
+ * threads, so they equal this serial loop bit for bit. */
+int or_lm_head_logits(const float *last_hidden, size_t hidden_len, const void *table, int dtype,
+                      size_t vocab_size, size_t hidden, float *logits);
+/* ops.rs:309-324 sample_argmax */
+int or_sample_argmax(const float *logits, size_t n, size_t *out);
+/* ops.rs:326-348 sample_argmax_excluding; has_excluded == 0 is Option::None */
+int or_sample_argmax_excluding(const float *logits, size_t n, int has_excluded, size_t excluded,
+                               size_t *out);
 int or_gemma_qk_prologue(float *q, size_t q_len, float *k, size_t k_len, size_t seq_len,
                          size_t q_heads, size_t kv_heads, size_t head_dim, const float *q_norm,
                          const float *k_norm, float eps, float rope_base,

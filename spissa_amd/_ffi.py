@@ -158,6 +158,10 @@ SIGNATURES = {
         C.c_int, [c_void_p, c_float_p, c_size, c_float_p, c_size, C.POINTER(LinearConfigC), c_float_p,
                   c_size]),
     "spissa_linear_device": (C.c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size, c_void_p]),
+    "spissa_lm_head_logits": (C.c_int, [c_void_p, c_float_p, c_size, c_float_p, c_size]),
+    "spissa_sample_argmax": (C.c_int, [c_void_p, c_float_p, c_size, C.c_int64, C.POINTER(c_size)]),
+    "spissa_argmax_device": (C.c_int, [c_void_p, c_void_p, c_size, C.c_int64, c_void_p]),
+    "spissa_lm_head_device": (C.c_int, [c_void_p, c_void_p, c_void_p, C.c_int64, c_void_p, c_void_p]),
     "spissa_attention_sublayer_device": (
         C.c_int, [c_void_p, C.POINTER(AttentionLayerC), c_void_p, c_size, c_void_p, c_void_p]),
 }

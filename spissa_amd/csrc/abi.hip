@@ -79,6 +79,7 @@ struct spissa_session {
   DevBuf table;     // drop-in RoPE rows
   DevBuf ppart;     // prefill key-split partials (O, then (m, l))
   DevBuf sub;       // attention sublayer intermediates (normed x, q, k, v, attention, projection)
+  DevBuf amax;      // argmax partials
   int cus = 256;    // compute units of the device
   // Buffers replaced by larger ones. They stay allocated until the session
   // is destroyed, so a HIP graph captured before a workspace grew still
@@ -166,6 +167,7 @@ static void session_free(spissa_session *s) {
   free_buf(s->table);
   free_buf(s->ppart);
   free_buf(s->sub);
+  free_buf(s->amax);
   for (void *p : s->retired) (void)hipFree(p);
   if (s->d_err) (void)hipFree(s->d_err);
   if (s->own_stream) (void)hipStreamDestroy(s->stream);
@@ -1207,7 +1209,8 @@ extern "C" int spissa_linear_weight_new(spissa_session *s, int dtype, size_t out
   w->in_features = in_features;
   HIP_TRY(hipSetDevice(s->device));
   HIP_TRY(hipMalloc(&w->data, data_bytes));
-  hipError_t e = hipMemcpyAsync(w->data, data, data_bytes, hipMemcpyHostToDevice, s->stream);
+  // host or device source: the runtime resolves the direction from the pointer
+  hipError_t e = hipMemcpyAsync(w->data, data, data_bytes, hipMemcpyDefault, s->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
   if (e != hipSuccess) {
     (void)hipFree(w->data);
@@ -1290,6 +1293,93 @@ extern "C" int spissa_linear_device(spissa_session *s, const spissa_linear_weigh
     return set_err(SPISSA_ERR_ARGUMENT, "weight lives on device %d, session on %d", w->session->device, s->device);
   if (batch && (!d_input || !d_out)) return set_err(SPISSA_ERR_ARGUMENT, "null buffer");
   return linear_launch(s, w, d_input, d_bias, batch, d_out);
+  GUARD_END
+}
+
+// ------------------------------------------------------------------------
+// LM head and greedy sampling (streaming/mod.rs:186-287, ops.rs:309-348)
+// ------------------------------------------------------------------------
+static int argmax_launch(spissa_session *s, const float *d_x, size_t n, int64_t excluded, int *d_token) {
+  if (n == 0) return set_err(SPISSA_ERR_INVALID_TENSOR_DATA, "cannot sample from empty logits");
+  if (n > (size_t)INT32_MAX - 1024) return set_err(SPISSA_ERR_SHAPE, "%zu logits exceed the device index range", n);
+  // ops.rs:326-332: no exclusion, an out-of-range one, or a single logit is
+  // plain sample_argmax
+  const int excl = (excluded < 0 || (uint64_t)excluded >= n || n <= 1) ? -1 : (int)excluded;
+  ST_TRY(ensure_buf(s, s->amax, kArgmaxMaxParts * sizeof(ArgmaxPart), false));
+  HIP_TRY(hipSetDevice(s->device));
+  HIP_TRY(launch_argmax(s->stream, d_x, (int)n, excl, (ArgmaxPart *)s->amax.p, d_token));
+  return SPISSA_OK;
+}
+
+static int check_lm_table(const spissa_linear_weight *t) {
+  if (!t) return set_err(SPISSA_ERR_ARGUMENT, "table is null");
+  if (t->dtype != SPISSA_DTYPE_F32 && t->dtype != SPISSA_DTYPE_BF16)
+    return set_err(SPISSA_ERR_INVALID_TENSOR_DATA, "LM head table must be f32 or bf16 (dtype %d)", t->dtype);
+  return SPISSA_OK;
+}
+
+extern "C" int spissa_lm_head_logits(const spissa_linear_weight *table, const float *last_hidden,
+                                     size_t last_hidden_len, float *logits, size_t logits_len) {
+  GUARD_BEGIN
+  ST_TRY(check_lm_table(table));
+  if (last_hidden_len != table->in_features)
+    return set_err(SPISSA_ERR_SHAPE, "last_hidden holds %zu floats, hidden is %zu", last_hidden_len,
+                   table->in_features);
+  if (logits_len != table->out_features)
+    return set_err(SPISSA_ERR_SHAPE, "logits hold %zu floats, vocab_size is %zu", logits_len, table->out_features);
+  if (!last_hidden || !logits) return set_err(SPISSA_ERR_ARGUMENT, "null buffer");
+  spissa_session *s = table->session;
+  float *r[2];
+  ST_TRY(io_regions(s, {last_hidden_len, logits_len}, r));
+  HIP_TRY(hipSetDevice(s->device));
+  ST_TRY(h2d(s, r[0], last_hidden, last_hidden_len * sizeof(float)));
+  ST_TRY(linear_launch(s, table, r[0], nullptr, 1, r[1]));
+  ST_TRY(d2h(s, logits, r[1], logits_len * sizeof(float)));
+  return sync_stream(s);
+  GUARD_END
+}
+
+extern "C" int spissa_sample_argmax(spissa_session *s, const float *logits, size_t n, int64_t excluded,
+                                    size_t *token) {
+  GUARD_BEGIN
+  if (!s || !token) return set_err(SPISSA_ERR_ARGUMENT, "null argument");
+  if (n == 0) return set_err(SPISSA_ERR_INVALID_TENSOR_DATA, "cannot sample from empty logits");
+  if (!logits) return set_err(SPISSA_ERR_ARGUMENT, "logits are null");
+  float *r[2];
+  ST_TRY(io_regions(s, {n, 1}, r));
+  HIP_TRY(hipSetDevice(s->device));
+  ST_TRY(h2d(s, r[0], logits, n * sizeof(float)));
+  ST_TRY(argmax_launch(s, r[0], n, excluded, reinterpret_cast<int *>(r[1])));
+  int t = -1;
+  ST_TRY(d2h(s, &t, r[1], sizeof(int)));
+  ST_TRY(sync_stream(s));
+  *token = (size_t)t;
+  return SPISSA_OK;
+  GUARD_END
+}
+
+extern "C" int spissa_argmax_device(spissa_session *s, const float *d_logits, size_t n, int64_t excluded,
+                                    int32_t *d_token) {
+  GUARD_BEGIN
+  if (!s) return set_err(SPISSA_ERR_ARGUMENT, "session is null");
+  if (n && (!d_logits || !d_token)) return set_err(SPISSA_ERR_ARGUMENT, "null buffer");
+  return argmax_launch(s, d_logits, n, excluded, d_token);
+  GUARD_END
+}
+
+extern "C" int spissa_lm_head_device(spissa_session *s, const spissa_linear_weight *table, const float *d_hidden,
+                                     int64_t excluded, float *d_logits, int32_t *d_token) {
+  GUARD_BEGIN
+  if (!s) return set_err(SPISSA_ERR_ARGUMENT, "session is null");
+  ST_TRY(check_lm_table(table));
+  if (table->session->device != s->device)
+    return set_err(SPISSA_ERR_ARGUMENT, "table lives on device %d, session on %d", table->session->device, s->device);
+  if (!d_hidden || !d_logits) return set_err(SPISSA_ERR_ARGUMENT, "null buffer");
+  if (d_token && table->out_features > (size_t)INT32_MAX - 1024)
+    return set_err(SPISSA_ERR_SHAPE, "%zu logits exceed the device index range", table->out_features);
+  ST_TRY(linear_launch(s, table, d_hidden, nullptr, 1, d_logits));
+  if (d_token) ST_TRY(argmax_launch(s, d_logits, table->out_features, excluded, d_token));
+  return SPISSA_OK;
   GUARD_END
 }
 

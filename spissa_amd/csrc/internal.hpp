@@ -152,6 +152,19 @@ hipError_t launch_generic(hipStream_t st, const GenericArgs &a);
 int linear_path(int dtype, long M, long K);
 hipError_t launch_linear(hipStream_t st, const LinearArgs &a, int path);
 
+// Greedy token choice: one partial per contiguous range of the logits.
+struct ArgmaxPart {
+  float v;       // first maximum of the range's non-NaN, non-excluded values
+  int i;         // its index (INT_MAX: the range has none)
+  int last_nan;  // last NaN index of the range (-1: none)
+  int pad;
+};
+constexpr int kArgmaxMaxParts = 1024;  // partials one launch writes at most
+// token[0] = sample_argmax(x[0..n)) for excl < 0, else
+// sample_argmax_excluding(x, excl) with 0 <= excl < n and n >= 2;
+// n <= INT32_MAX - 1024.
+hipError_t launch_argmax(hipStream_t st, const float *x, int n, int excl, ArgmaxPart *parts, int *token);
+
 // Keys per split of a decode launch: total_rows = key rows summed over all
 // (sequence, KV head, head block) triples; max_keys = longest visible range.
 int decode_keys_per_split(int D, int RB, long total_rows, int max_keys);

@@ -29,6 +29,18 @@ def _dev(t, name: str) -> int:
     return t.data_ptr()
 
 
+def _dev_i32(t, name: str) -> int:
+    if t is None:
+        return 0
+    if not getattr(t, "is_cuda", False):
+        raise TypeError(f"{name} must be a device tensor")
+    import torch
+
+    if t.dtype != torch.int32 or t.numel() < 1:
+        raise TypeError(f"{name} must be an int32 tensor with at least one element")
+    return t.data_ptr()
+
+
 class RopeTable:
     """A resident cos/sin table (spissa_rope_table_new)."""
 
@@ -221,3 +233,16 @@ class Session:
         """out[batch, out] = x[batch, in] x W^T + bias on device tensors (bias may be None)."""
         check(self._lib.spissa_linear_device(self.handle, weight.handle, _dev(x, "x"),
                                              _dev(bias, "bias") or None, batch, _dev(out, "out")))
+
+    def argmax(self, logits, n: int, token, excluded: Optional[int] = None) -> None:
+        """token[0] (int32 device tensor) = sample_argmax(logits[:n]) for excluded None, else
+        sample_argmax_excluding(logits[:n], excluded) (ops.rs:309-348)."""
+        check(self._lib.spissa_argmax_device(self.handle, _dev(logits, "logits"), n,
+                                             -1 if excluded is None else excluded, _dev_i32(token, "token")))
+
+    def lm_head(self, table, hidden, logits, token=None, excluded: Optional[int] = None) -> None:
+        """logits [vocab] = table x hidden [hidden] (streaming/mod.rs:186-287), then, with a token
+        tensor, its argmax as in argmax()."""
+        check(self._lib.spissa_lm_head_device(self.handle, table.handle, _dev(hidden, "hidden"),
+                                              -1 if excluded is None else excluded, _dev(logits, "logits"),
+                                              _dev_i32(token, "token")))

@@ -58,23 +58,32 @@ class LinearWeight:
     """A [out_features, in_features] weight resident in HBM.
 
     data: float32 array (DTYPE_F32) or uint16 array of bf16 / binary16 bits
-    (DTYPE_BF16 / DTYPE_F16), row-major, out_features * in_features elements.
+    (DTYPE_BF16 / DTYPE_F16), row-major, out_features * in_features elements;
+    or a contiguous device tensor of the same bytes (float32, or a 16-bit
+    dtype), copied device to device after the current stream's work.
     """
 
-    def __init__(self, data: np.ndarray, dtype: int, out_features: int, in_features: int,
-                 session=None):
+    def __init__(self, data, dtype: int, out_features: int, in_features: int, session=None):
         lib = _ffi.load()
         self._lib = lib
-        want = np.float32 if dtype == DTYPE_F32 else np.uint16
-        if data.dtype != want or not data.flags.c_contiguous:
-            raise TypeError(f"weight data must be a contiguous {np.dtype(want).name} array")
+        if getattr(data, "is_cuda", False):
+            import torch
+
+            ok = data.dtype == torch.float32 if dtype == DTYPE_F32 else data.element_size() == 2
+            if not ok or not data.is_contiguous():
+                raise TypeError("device weight data must be a contiguous tensor of the dtype's width")
+            torch.cuda.current_stream(data.device).synchronize()
+            ptr, nbytes = _ffi.c_void_p(data.data_ptr()), data.numel() * data.element_size()
+        else:
+            want = np.float32 if dtype == DTYPE_F32 else np.uint16
+            if data.dtype != want or not data.flags.c_contiguous:
+                raise TypeError(f"weight data must be a contiguous {np.dtype(want).name} array")
+            ptr, nbytes = data.ctypes.data_as(_ffi.c_void_p), data.nbytes
         s = session.handle if session is not None else self._default_session(lib)
         # the weight is freed through its session: keep the session alive as long
         self._session = session
         h = _ffi.c_void_p()
-        check(lib.spissa_linear_weight_new(s, dtype, out_features, in_features,
-                                           data.ctypes.data_as(_ffi.c_void_p), data.nbytes,
-                                           C.byref(h)))
+        check(lib.spissa_linear_weight_new(s, dtype, out_features, in_features, ptr, nbytes, C.byref(h)))
         self._h = h
         self.dtype, self.out_features, self.in_features = dtype, out_features, in_features
 

@@ -438,6 +438,155 @@ TEST(linear_rejects_mismatched_shapes_and_bytes) {
   CHECK(bad_bytes.is_err() && bad_bytes.error().kind == ErrorKind::InvalidTensorData);
 }
 
+// ------------------------------------------- LM head and greedy sampling
+
+// ops.rs:570-573
+TEST(sample_argmax_is_deterministic) { CHECK(ok(sample_argmax(std::vector<float>{0.1f, 2.0f, 1.9f})) == 1); }
+
+// ops.rs:575-586
+TEST(sample_argmax_excluding_uses_next_best_token) {
+  CHECK(ok(sample_argmax_excluding(std::vector<float>{0.1f, 2.0f, 1.9f}, 1)) == 2);
+  CHECK(ok(sample_argmax_excluding(std::vector<float>{0.1f, 2.0f, 1.9f}, 99)) == 1);
+  CHECK(ok(sample_argmax_excluding(std::vector<float>{2.0f}, 0)) == 0);
+}
+
+// ops.rs:309-314: empty logits are InvalidTensorData
+TEST(sample_argmax_rejects_empty_logits) {
+  auto r = sample_argmax(std::vector<float>{});
+  CHECK(r.is_err() && r.error().kind == ErrorKind::InvalidTensorData);
+  CHECK(r.error().message.find("cannot sample from empty logits") != std::string::npos);
+}
+
+static size_t first_argmax(const std::vector<float> &v) {
+  size_t best = 0;
+  for (size_t i = 1; i < v.size(); ++i)
+    if (v[i] > v[best]) best = i;
+  return best;
+}
+
+// streaming/tests.rs:303-327: the LM head over an f32 table equals the serial
+// left-to-right loop bit for bit (hidden 5 runs the device's sequential kernel)
+TEST(r131_parallel_lm_head_matches_serial_bit_for_bit) {
+  const size_t hidden = 5, vocab = 37;
+  std::vector<float> last_hidden(hidden), weight(vocab * hidden);
+  for (size_t h = 0; h < hidden; ++h) last_hidden[h] = std::sin((float)h * 0.37f - 0.5f);
+  for (size_t i = 0; i < weight.size(); ++i) weight[i] = std::cos((float)i * 0.013f - 0.21f) * 0.5f;
+  auto table = ok(LinearWeight::create(DType::F32, vocab, hidden, weight.data(), weight.size() * 4));
+  auto parallel = ok(lm_head_logits_parallel(last_hidden, table, vocab, hidden));
+  std::vector<float> serial(vocab);
+  for (size_t v = 0; v < vocab; ++v) {
+    float sum = 0.0f;
+    for (size_t h = 0; h < hidden; ++h) sum += last_hidden[h] * weight[v * hidden + h];
+    serial[v] = sum;
+  }
+  CHECK(std::memcmp(parallel.data(), serial.data(), vocab * 4) == 0);
+}
+
+// streaming/tests.rs:329-366: the bf16 table agrees with the f32 table of its
+// exact upcast within 1e-4, with the same argmax
+TEST(lm_head_bf16_direct_matches_f32_upcast_within_accumulation_tolerance) {
+  const size_t hidden = 5, vocab = 37;
+  std::vector<float> last_hidden(hidden), f32_weight(vocab * hidden);
+  std::vector<uint16_t> bits(vocab * hidden);
+  for (size_t h = 0; h < hidden; ++h) last_hidden[h] = std::cos((float)h * 0.41f - 0.6f);
+  for (size_t i = 0; i < bits.size(); ++i) {
+    const float v = std::sin((float)i * 0.017f - 0.3f) * 0.5f;
+    uint32_t u;
+    std::memcpy(&u, &v, 4);
+    bits[i] = (uint16_t)(u >> 16);
+    const uint32_t up = (uint32_t)bits[i] << 16;
+    std::memcpy(&f32_weight[i], &up, 4);
+  }
+  auto tb = ok(LinearWeight::create(DType::Bf16, vocab, hidden, bits.data(), bits.size() * 2));
+  auto tf = ok(LinearWeight::create(DType::F32, vocab, hidden, f32_weight.data(), f32_weight.size() * 4));
+  auto from_bf16 = ok(lm_head_logits_parallel_bf16(last_hidden, tb, vocab, hidden));
+  auto from_f32 = ok(lm_head_logits_parallel(last_hidden, tf, vocab, hidden));
+  float max_abs_diff = 0.0f;
+  for (size_t v = 0; v < vocab; ++v) max_abs_diff = std::fmax(max_abs_diff, std::fabs(from_bf16[v] - from_f32[v]));
+  CHECK(max_abs_diff < 1e-4f);
+  CHECK(first_argmax(from_bf16) == first_argmax(from_f32));
+  CHECK(ok(sample_argmax(from_bf16)) == first_argmax(from_bf16));
+}
+
+// streaming/tests.rs:4093-4153: Gemma 3 4B hidden, vocab 257, xorshift data;
+// within 1e-2 of the scalar reference and the same argmax
+TEST(lm_head_bf16_simd_matches_scalar_reference_and_preserves_argmax) {
+  const size_t hidden = 2560, vocab = 257;
+  uint64_t state = 0x9e3779b97f4a7c15ull;
+  auto next = [&]() {
+    state ^= state << 13;
+    state ^= state >> 7;
+    state ^= state << 17;
+    return (float)(state >> 40) / 16777216.0f - 0.5f;
+  };
+  std::vector<float> last_hidden(hidden), weight_vals(vocab * hidden);
+  for (auto &x : last_hidden) x = next() * 2.0f;
+  std::vector<uint16_t> bits(vocab * hidden);
+  for (size_t i = 0; i < bits.size(); ++i) {
+    const float v = next();
+    uint32_t u;
+    std::memcpy(&u, &v, 4);
+    bits[i] = (uint16_t)(u >> 16);
+    const uint32_t up = (uint32_t)bits[i] << 16;
+    std::memcpy(&weight_vals[i], &up, 4);
+  }
+  auto table = ok(LinearWeight::create(DType::Bf16, vocab, hidden, bits.data(), bits.size() * 2));
+  auto logits = ok(lm_head_logits_parallel_bf16(last_hidden, table, vocab, hidden));
+  std::vector<float> reference(vocab);
+  for (size_t row = 0; row < vocab; ++row) {
+    float sum = 0.0f;
+    for (size_t h = 0; h < hidden; ++h) sum += last_hidden[h] * weight_vals[row * hidden + h];
+    reference[row] = sum;
+  }
+  float max_abs_diff = 0.0f;
+  for (size_t v = 0; v < vocab; ++v) max_abs_diff = std::fmax(max_abs_diff, std::fabs(logits[v] - reference[v]));
+  CHECK(max_abs_diff < 1e-2f);
+  CHECK(first_argmax(logits) == first_argmax(reference));
+  CHECK(ok(sample_argmax(logits)) == first_argmax(logits));
+}
+
+// The device tail (logits and token in one call) against the drop-in calls.
+TEST(device_lm_head_token_matches_dropin_argmax) {
+  const size_t hidden = 1152, vocab = 20000;
+  std::vector<uint16_t> bits(vocab * hidden);
+  std::vector<float> x(hidden);
+  uint64_t state = 0x243f6a8885a308d3ull;
+  auto next = [&]() {
+    state ^= state << 13;
+    state ^= state >> 7;
+    state ^= state << 17;
+    return (float)(state >> 40) / 16777216.0f - 0.5f;
+  };
+  for (auto &b : bits) {
+    const float v = next() * 0.1f;
+    uint32_t u;
+    std::memcpy(&u, &v, 4);
+    b = (uint16_t)(u >> 16);
+  }
+  for (auto &v : x) v = next();
+  auto sess = ok(Session::create());
+  auto table = ok(sess.linear_weight(DType::Bf16, vocab, hidden, bits.data(), bits.size() * 2));
+  float *d_x = nullptr, *d_logits = nullptr;
+  int32_t *d_tok = nullptr;
+  CHECK(hipMalloc(&d_x, hidden * 4) == hipSuccess && hipMalloc(&d_logits, vocab * 4) == hipSuccess &&
+        hipMalloc(&d_tok, 4) == hipSuccess);
+  CHECK(hipMemcpy(d_x, x.data(), hidden * 4, hipMemcpyHostToDevice) == hipSuccess);
+  auto host = ok(lm_head_logits_parallel_bf16(x, table, vocab, hidden));
+  for (std::optional<size_t> excl : {std::optional<size_t>{}, std::optional<size_t>{first_argmax(host)}}) {
+    ok(sess.lm_head(table, d_x, d_logits, d_tok, excl));
+    ok(sess.sync());
+    std::vector<float> logits(vocab);
+    int32_t tok = -1;
+    CHECK(hipMemcpy(logits.data(), d_logits, vocab * 4, hipMemcpyDeviceToHost) == hipSuccess);
+    CHECK(hipMemcpy(&tok, d_tok, 4, hipMemcpyDeviceToHost) == hipSuccess);
+    CHECK(std::memcmp(logits.data(), host.data(), vocab * 4) == 0);
+    CHECK((size_t)tok == ok(sample_argmax_excluding(logits, excl)));
+  }
+  (void)hipFree(d_x);
+  (void)hipFree(d_logits);
+  (void)hipFree(d_tok);
+}
+
 // models/llama/generate.rs:200-450 on the device in one call equals the same
 // sequence through the drop-in API: rms_norm, three projections, RoPE at the
 // cache's next position, cached attention, append, o projection.
