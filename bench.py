@@ -577,7 +577,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(d1["attn_kernel_GBps"] / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic(),
-            "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, calibrated on a 256 MiB copy "
+            "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, calibrated on copies of known size "
                               "(profiles/decode_b1_hbm_traffic.md)",
             "kernel": "one decode attention launch = decode_split_kernel<128,3,3> + decode_combine_kernel<128,3>; "
                       "event-timed average over 28 back-to-back launches per graph replay",
