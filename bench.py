@@ -288,6 +288,8 @@ def gpu_bench(args) -> dict:
             res["projections"] = projection_bench(sess, stream, gen, dev, args, time_graph)
             log("timing the LM head")
             res["lm_head"] = lm_head_bench(sess, stream, gen, dev, args, time_graph)
+            log("timing the other BASELINE configs")
+            res["configs"] = configs_bench(sess, stream, gen, dev, args, time_graph)
     return res
 
 
@@ -436,6 +438,107 @@ def lm_head_bench(sess, stream, gen, dev, args, time_graph) -> dict:
         rec["table_bytes"] = tbytes
         out[name] = rec
         del tables, x, logits, tok
+        torch.cuda.empty_cache()
+    return out
+
+
+# The attention layers of the other BASELINE configs, each measured over
+# `layers` distinct caches (more than the 256 MB last-level cache holds, where
+# the reads are large enough to matter):
+# (name, BASELINE config, layers, Hq, Hkv, d, query rows S, cached rows P, window, llama RoPE)
+CONFIG_CASES = [
+    ("llama32_1b_decode_512", 0, 16, 32, 8, 64, 1, 512, 0, True),
+    ("llama32_1b_prefill_2048", 1, 16, 32, 8, 64, 2048, 0, 0, False),
+    ("llama32_1b_decode_2048", 1, 16, 32, 8, 64, 1, 2048, 0, True),
+    ("gemma3_1b_prefill_4096_global", 3, 4, 4, 1, 256, 4096, 0, 0, False),
+    ("gemma3_1b_prefill_4096_local_w512", 3, 8, 4, 1, 256, 4096, 0, 512, False),
+    ("gemma3_1b_decode_32768_global", 3, 8, 4, 1, 256, 1, 32768, 0, False),
+    ("gemma3_1b_decode_32768_local_w512", 3, 8, 4, 1, 256, 1, 32768, 512, False),
+    ("gemma3_4b_chunk_128_on_16384_global", 4, 5, 8, 4, 256, 128, 16384, 0, False),
+    ("gemma3_4b_chunk_128_on_16384_local_w1024", 4, 8, 8, 4, 256, 128, 16384, 1024, False),
+    ("gemma3_4b_decode_16512_global", 4, 5, 8, 4, 256, 1, 16512, 0, False),
+    ("gemma3_4b_decode_16512_local_w1024", 4, 8, 8, 4, 256, 1, 16512, 1024, False),
+]
+
+
+def visible_pairs(S: int, P: int, window: int) -> int:
+    """Unmasked (query, key) pairs of a causal chunk of S rows after P cached rows."""
+    total = 0
+    for i in range(S):
+        k = P + i + 1
+        total += min(k, window) if window > 0 else k
+    return total
+
+
+def configs_bench(sess, stream, gen, dev, args, time_graph) -> dict:
+    """One record per case of CONFIG_CASES: decode layers as the fused step
+    (RoPE for the Llama shapes, attention, append), prefill and chunk layers
+    as the attention call. Work is credited by the algorithmic figures: decode
+    bytes of the visible keys, prefill FLOP of the unmasked pairs; chunks also
+    report the bytes of their visible f32 K/V."""
+    import torch
+
+    from spissa_amd import _ffi
+    from spissa_amd.rotary import KvAttentionConfig
+
+    out = {}
+    for name, cfg_id, L, hq, hkv, d, S, P, W, rope in CONFIG_CASES:
+        w = hkv * d
+        with torch.cuda.stream(stream):
+            caches = []
+            for l in range(L):
+                gen.manual_seed(5000 + 100 * cfg_id + l)
+                c = sess.kv_cache(hkv, d, P + S) if P > 0 or S == 1 else None
+                if P > 0:
+                    sess.append(c, torch.randn(P * w, generator=gen, device=dev),
+                                torch.randn(P * w, generator=gen, device=dev), P)
+                caches.append(c)
+            q = [torch.randn(S * hq * d, generator=gen, device=dev) for _ in range(L)]
+            k = [torch.randn(S * w, generator=gen, device=dev) for _ in range(L)]
+            v = [torch.randn(S * w, generator=gen, device=dev) for _ in range(L)]
+            o = [torch.empty(S * hq * d, device=dev) for _ in range(L)]
+        table = sess.rope_table(_ffi.ROPE_LLAMA, d, THETA, max_positions=P + S + 64) if rope else None
+        cfg = KvAttentionConfig(S, hq, hkv, d, True, W)
+        decode = S == 1
+
+        def step():
+            for l in range(L):
+                if decode:
+                    sess.decode_step(table, q[l], k[l], v[l], [caches[l]], cfg, o[l])
+                else:
+                    sess.attention(q[l], k[l], v[l], caches[l], cfg, o[l])
+
+        def reset():
+            if decode:
+                for c in caches:
+                    c.truncate(P)
+
+        step()
+        sess.sync()
+        reset()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            step()
+        reset()
+        ms = time_graph(g, max(3, args.steps // 4), 2)
+        us = ms * 1e3 / L
+        rec = {"config": cfg_id, "layers": L, "us_per_layer": round(us, 3)}
+        if decode:
+            keys = min(P + 1, W) if W > 0 else P + 1
+            nbytes = decode_bytes(keys, hq, hkv, d)
+            rec.update(GBps=round(nbytes / (us * 1e-6) / 1e9, 1),
+                       hbm_frac=round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), bytes_per_layer=nbytes)
+        else:
+            fl = 4.0 * d * hq * visible_pairs(S, P, W)
+            rec.update(TFLOPs=round(fl / (us * 1e-6) / 1e12, 2),
+                       mfma_frac=round(fl / (us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4), flop_per_layer=fl)
+            if P > 0:
+                keys = min(P + S, W + S) if W > 0 else P + S
+                nbytes = keys * w * 8 + 2 * S * hq * d * 4
+                rec.update(GBps=round(nbytes / (us * 1e-6) / 1e9, 1),
+                           hbm_frac=round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4))
+        out[name] = rec
+        del g, caches, q, k, v, o, table
         torch.cuda.empty_cache()
     return out
 
@@ -607,6 +710,12 @@ def main() -> int:
                                        "table (logits GEMV) + argmax token; token_us = both, logits_us = GEMV "
                                        "only, argmax_us = argmax only",
                            **res["lm_head"]}
+    if "configs" in res:
+        line["configs"] = {"workload": "attention layers of the other BASELINE configs (index into "
+                                       "BASELINE.json configs): decode = fused RoPE/attention/append step, "
+                                       "prefill and chunk = the attention call; GB/s and TFLOP/s from the "
+                                       "algorithmic bytes and unmasked pairs",
+                           **res["configs"]}
     if cpu is not None:
         line["cpu_baseline"] = cpu
     print(json.dumps(line), flush=True)

@@ -1025,7 +1025,7 @@ static int run_prefill(spissa_session *s, const float *d_q, const float *d_k, co
     if (a.window > 0) keys = std::min(keys, (long)a.window + wgq + bn);
     const long tiles = (keys + bn - 1) / bn + 1;
     const long want = std::min(std::min((slots + base - 1) / base, tiles / 4), (long)D);
-    if (want >= 2) {  // (the combine kernel merges at most head_dim splits)
+    if (want >= 2) {  // (at most head_dim splits: the measured useful range)
       a.tps = (int)((tiles + want - 1) / want);
       a.splits = (int)((tiles + a.tps - 1) / a.tps);
       const size_t rows = (size_t)a.splits * S * a.Hq;

@@ -535,60 +535,100 @@ long prefill_base_workgroups(const PrefillArgs &a, int D) {
 
 // Merges key splits: per (query row, head), M = max m_j, then
 // O = sum_j O_j 2^(m_j - M), L = sum_j l_j 2^(m_j - M), out = O / L. Splits
-// that saw no key of the row (m_j = -inf) contribute nothing. One workgroup of
-// D threads per (row, head): the (m, l) pairs of all splits are loaded once
-// into LDS by parallel threads, then every thread accumulates its output
-// element over the splits with independent loads. The error bit is set for an
-// invalid L, as the unsplit kernels do (rotary.rs:560-564).
+// that saw no key of the row (m_j = -inf) contribute nothing. WPR waves share
+// a row (WPR = 1: four rows per workgroup; WPR = 4: one): lane l holds the
+// row's elements [l * D/64, (l + 1) * D/64), the lanes find M together, and
+// wave w sums splits w, w + WPR, ... in order, reading each split's (m, l)
+// pair on every lane (one line per split). With WPR = 4 the four partial sums
+// meet in LDS, in wave order. The error bit is set for an invalid L, as the
+// unsplit kernels do (rotary.rs:560-564).
 constexpr int kMaxPrefillSplits = 256;
+// Above this many splits a row gets a whole workgroup.
+constexpr int kCombineWaveSplits = 8;
 
-__global__ __launch_bounds__(256) void prefill_combine_kernel(const PrefillArgs a, int D) {
-  __shared__ float s_g[kMaxPrefillSplits];  // weight 2^(m_j - M) (0 for empty splits)
-  __shared__ float s_l[kMaxPrefillSplits];
-  __shared__ float s_red[256];
-  const long row = blockIdx.x;  // pos * Hq + head
-  const int d = threadIdx.x;
-  const long stride = (long)a.S * a.Hq;
-  float mj = -__builtin_inff(), lj = 0.0f;
-  for (int j = d; j < a.splits; j += blockDim.x) {  // splits <= kMaxPrefillSplits <= blockDim in practice
-    mj = a.part_ml[(j * stride + row) * 2];
-    lj = a.part_ml[(j * stride + row) * 2 + 1];
+template <int E>
+__device__ __forceinline__ void load_e(const float *p, float (&v)[E]) {
+  if constexpr (E == 4) {
+    const float4 q = *reinterpret_cast<const float4 *>(p);
+    v[0] = q.x, v[1] = q.y, v[2] = q.z, v[3] = q.w;
+  } else if constexpr (E == 2) {
+    const float2 q = *reinterpret_cast<const float2 *>(p);
+    v[0] = q.x, v[1] = q.y;
+  } else {
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[e] = p[e];
   }
-  s_red[d] = mj;
-  __syncthreads();
-  for (int w = blockDim.x / 2; w > 0; w >>= 1) {
-    if (d < w) s_red[d] = fmaxf(s_red[d], s_red[d + w]);
-    __syncthreads();
-  }
-  const float M = s_red[0];
+}
+
+template <int D, int WPR>
+__global__ __launch_bounds__(256) void prefill_combine_kernel(const PrefillArgs a) {
+  constexpr int E = D / 64;
+  __shared__ float s_o[WPR > 1 ? WPR : 1][64][E];
+  __shared__ float s_l[WPR > 1 ? WPR : 1];
+  const long rows = (long)a.S * a.Hq;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const long row = (long)blockIdx.x * (4 / WPR) + wave / WPR;  // pos * Hq + head
+  const int sub = wave % WPR;
+  if (WPR == 1 && row >= rows) return;  // whole waves; with WPR > 1 the grid is exact
+  const float *ml = a.part_ml + row * 2;  // split j at ml[j * rows * 2]
+  float M = -__builtin_inff();
+  for (int j = lane; j < a.splits; j += 64) M = fmaxf(M, ml[j * rows * 2]);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
   const float Ms = M == -__builtin_inff() ? 0.0f : M;
-  if (d < a.splits) {
-    s_g[d] = mj == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(mj - Ms);
-    s_l[d] = lj;
+  float L = 0.0f, O[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) O[e] = 0.0f;
+  const float *po = a.part_o + row * D + lane * E;
+#pragma unroll 8
+  for (int j = sub; j < a.splits; j += WPR) {
+    const float mj = ml[j * rows * 2], lj = ml[j * rows * 2 + 1];
+    const float g = mj == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(mj - Ms);
+    float o[E];
+    load_e<E>(po + j * rows * D, o);
+#pragma unroll
+    for (int e = 0; e < E; ++e) O[e] = fmaf(o[e], g, O[e]);
+    L = fmaf(lj, g, L);
   }
-  __syncthreads();
-  float L = 0.0f, O = 0.0f;
-  const float *po = a.part_o + row * D + d;
-  int j = 0;
-  for (; j + 4 <= a.splits; j += 4) {  // four independent loads in flight
-    const float o0 = po[(j + 0) * stride * D], o1 = po[(j + 1) * stride * D];
-    const float o2 = po[(j + 2) * stride * D], o3 = po[(j + 3) * stride * D];
-    O = fmaf(o0, s_g[j], O);
-    O = fmaf(o1, s_g[j + 1], O);
-    O = fmaf(o2, s_g[j + 2], O);
-    O = fmaf(o3, s_g[j + 3], O);
+  if constexpr (WPR > 1) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) s_o[sub][lane][e] = O[e];
+    if (lane == 0) s_l[sub] = L;
+    __syncthreads();
+    if (sub != 0) return;
+#pragma unroll
+    for (int w = 1; w < WPR; ++w) {
+#pragma unroll
+      for (int e = 0; e < E; ++e) O[e] += s_o[w][lane][e];
+      L += s_l[w];
+    }
   }
-  for (; j < a.splits; ++j) O = fmaf(po[j * stride * D], s_g[j], O);
-  for (int k = 0; k < a.splits; ++k) L = fmaf(s_l[k], s_g[k], L);
-  a.out[row * D + d] = O / L;
-  if (d == 0 && !(__float_as_uint(L) - 1u < 0x7f7fffffu)) atomicOr(a.err, kDevErrSoftmaxDenominator);
+  float *dst = a.out + row * D + lane * E;
+#pragma unroll
+  for (int e = 0; e < E; ++e) dst[e] = O[e] / L;
+  if (lane == 0 && !(__float_as_uint(L) - 1u < 0x7f7fffffu)) atomicOr(a.err, kDevErrSoftmaxDenominator);
+}
+
+template <int D>
+hipError_t launch_combine_d(hipStream_t st, const PrefillArgs &a) {
+  const long rows = (long)a.S * a.Hq;
+  if (a.splits > kCombineWaveSplits) {
+    hipLaunchKernelGGL((prefill_combine_kernel<D, 4>), dim3((unsigned)rows), dim3(256), 0, st, a);
+  } else {
+    hipLaunchKernelGGL((prefill_combine_kernel<D, 1>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, a);
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_prefill_combine(hipStream_t st, const PrefillArgs &a, int D) {
   if (a.splits <= 1) return hipSuccess;
-  if (a.splits > kMaxPrefillSplits || a.splits > D) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(prefill_combine_kernel, dim3((unsigned)((long)a.S * a.Hq)), dim3(D), 0, st, a, D);
-  return hipGetLastError();
+  if (a.splits > kMaxPrefillSplits) return hipErrorInvalidValue;
+  switch (D) {
+    case 64: return launch_combine_d<64>(st, a);
+    case 128: return launch_combine_d<128>(st, a);
+    case 256: return launch_combine_d<256>(st, a);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_prefill(hipStream_t st, const PrefillArgs &a, int D) {
