@@ -184,18 +184,31 @@ __global__ __launch_bounds__(256) void stage_bf16_kernel(const float *__restrict
   const long lo = dst_first, hi = dst_first + n_pad;  // positions this call writes
 
   // K rows (and V rows into LDS): position P0 + r holds source row i = P0 + r - dst_first.
-  for (int w = threadIdx.x; w < 64 * 8; w += 256) {
+  // Both of a thread's rows are loaded before either is converted, so all
+  // eight 16-byte loads are in flight together.
+  float4 src[2][4];
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int w = threadIdx.x + 256 * it;
     const int r = w >> 3, cc = w & 7;
     const long pos = P0 + r, i = pos - dst_first;
-    if (pos < lo || pos >= hi) continue;
-    float4 k0 = make_float4(0.f, 0.f, 0.f, 0.f), k1 = k0, v0 = k0, v1 = k0;
-    if (i < n) {
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    src[it][0] = src[it][1] = src[it][2] = src[it][3] = z;
+    if (pos >= lo && pos < hi && i < n) {
       const long base = (i * H + h) * (long)D + d0 + 8 * cc;
-      k0 = *reinterpret_cast<const float4 *>(k_rows + base);
-      k1 = *reinterpret_cast<const float4 *>(k_rows + base + 4);
-      v0 = *reinterpret_cast<const float4 *>(v_rows + base);
-      v1 = *reinterpret_cast<const float4 *>(v_rows + base + 4);
+      src[it][0] = *reinterpret_cast<const float4 *>(k_rows + base);
+      src[it][1] = *reinterpret_cast<const float4 *>(k_rows + base + 4);
+      src[it][2] = *reinterpret_cast<const float4 *>(v_rows + base);
+      src[it][3] = *reinterpret_cast<const float4 *>(v_rows + base + 4);
     }
+  }
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int w = threadIdx.x + 256 * it;
+    const int r = w >> 3, cc = w & 7;
+    const long pos = P0 + r;
+    if (pos < lo || pos >= hi) continue;
+    const float4 k0 = src[it][0], k1 = src[it][1], v0 = src[it][2], v1 = src[it][3];
     bf16x8 kv;
     kv[0] = (bf16)k0.x; kv[1] = (bf16)k0.y; kv[2] = (bf16)k0.z; kv[3] = (bf16)k0.w;
     kv[4] = (bf16)k1.x; kv[5] = (bf16)k1.y; kv[6] = (bf16)k1.z; kv[7] = (bf16)k1.w;
