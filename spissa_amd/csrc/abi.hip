@@ -1019,11 +1019,11 @@ static int run_prefill(spissa_session *s, const float *d_q, const float *d_k, co
   // each covering at least four key tiles of its workgroup's range.
   const long base = prefill_base_workgroups(a, D);
   const long slots = (long)s->cus * prefill_wgs_per_cu(D);
+  const int bn = prefill_tile_keys(D), wgq = prefill_wg_queries(a, D);
+  long keys = (long)P + S;  // widest visible key range of one workgroup
+  if (a.window > 0) keys = std::min(keys, (long)a.window + wgq + bn);
+  const long tiles = (keys + bn - 1) / bn + 1;
   if (base < slots) {
-    const int bn = prefill_tile_keys(D), wgq = prefill_wg_queries(a, D);
-    long keys = (long)P + S;  // widest visible key range of one workgroup
-    if (a.window > 0) keys = std::min(keys, (long)a.window + wgq + bn);
-    const long tiles = (keys + bn - 1) / bn + 1;
     const long want = std::min(std::min((slots + base - 1) / base, tiles / 4), (long)D);
     if (want >= 2) {  // (at most head_dim splits: the measured useful range)
       a.tps = (int)((tiles + want - 1) / want);
@@ -1034,6 +1034,10 @@ static int run_prefill(spissa_session *s, const float *d_q, const float *d_k, co
       a.part_ml = a.part_o + rows * D;
     }
   }
+  // The O split where a workgroup covers at least 32 key tiles (measured:
+  // 10% faster on a 4096-token causal prefill at head_dim 256, 5-9% slower on
+  // windowed and split ranges of 10-19 tiles).
+  a.o_split = D >= 256 && (a.splits > 1 ? a.tps : tiles) >= 32;
   HIP_TRY(launch_prefill(s->stream, a, D));
   HIP_TRY(launch_prefill_combine(s->stream, a, D));
   return SPISSA_OK;

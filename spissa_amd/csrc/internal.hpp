@@ -103,6 +103,10 @@ struct PrefillArgs {
   // key); launch_prefill_combine merges them. splits == 1 writes `out`.
   int splits, tps;
   float *part_o, *part_ml;
+  // head_dim 256: split O over two waves per (head, query block). It costs
+  // 1.5x the MFMAs (both waves compute the scores) and doubles the waves per
+  // SIMD, which pays off on long key ranges per workgroup.
+  int o_split;
 };
 
 // Workgroup slots per CU and key-tile width of the prefill kernels, and the

@@ -143,16 +143,19 @@ __device__ __forceinline__ void score_tile(f32x16 (&s)[QB][BN / 32], const char 
 }  // namespace
 
 // QB query blocks of 32 per wave (1 or 2); two waves per SIMD unless the
-// accumulators need the whole register file (head_dim 256, or two 128-wide
-// blocks).
-template <int D, int RB, int NPB, int BN, int QB>
-__global__ __launch_bounds__(RB *NPB * 64, ((QB == 1 && D <= 128) || D <= 64) ? 2 : 1) void prefill_kernel(
-    const PrefillArgs a) {
-  constexpr int NW = RB * NPB;
+// accumulators need the whole register file (two 128-wide blocks).
+// OS: waves sharing one (head, query block), each holding D / OS columns of
+// O. With OS = 2 both compute the whole score tile and each accumulates its
+// half of O^T += V^T P^T: 1.5x the MFMAs, but half the O registers, which at
+// head_dim 256 lets two waves share a SIMD instead of one.
+template <int D, int RB, int NPB, int BN, int QB, int OS>
+__global__ __launch_bounds__(RB *NPB *OS * 64, (OS == 1 && ((QB == 1 && D <= 128) || D <= 64)) ? 2 : 1) void
+prefill_kernel(const PrefillArgs a) {
+  constexpr int NW = RB * NPB * OS;
   constexpr int WQ = QB * 32;  // queries per wave
   constexpr int WGQ = NPB * WQ;
   using G = Geom<D, BN, NW>;
-  constexpr int DT = G::DT, KB = G::KB, KS = G::KS, DB = G::DB;
+  constexpr int DT = G::DT, KB = G::KB, KS = G::KS, DB = G::DB / OS;  // DB: output blocks of this wave
 
   // Four separate LDS objects (not one array): the compiler then knows that
   // copies into one buffer do not alias reads of another and does not wait
@@ -173,7 +176,9 @@ __global__ __launch_bounds__(RB *NPB * 64, ((QB == 1 && D <= 128) || D <= 64) ? 
   // The wave index is uniform: readfirstlane keeps it (and all that derives
   // from it) in scalar registers and wave-level branches uniform.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int r = wave % RB, pb = wave / RB;
+  const int oh = wave / (RB * NPB);  // which D / OS columns of O this wave holds
+  const int r = wave % RB, pb = (wave / RB) % NPB;
+  const int d_base = oh * DB;
   const int head = h * a.R + hb * RB + r;
   const int p0 = qt * WGQ;
   const int wp0 = p0 + pb * WQ;
@@ -192,7 +197,7 @@ __global__ __launch_bounds__(RB *NPB * 64, ((QB == 1 && D <= 128) || D <= 64) ? 
   }
   if (t_begin >= t_end) {  // this split sees none of the workgroup's keys (uniform exit)
     const int pos = wp0 + lane;
-    if (lane < WQ && pos < a.S) {
+    if (lane < WQ && pos < a.S && oh == 0) {
       float *ml = a.part_ml + (((long)split * a.S + pos) * a.Hq + head) * 2;
       ml[0] = -__builtin_inff();
       ml[1] = 0.0f;
@@ -385,7 +390,7 @@ __global__ __launch_bounds__(RB *NPB * 64, ((QB == 1 && D <= 128) || D <= 64) ? 
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
       for (int d = 0; d < DB; ++d) {
-        const bf16x8 vf = *reinterpret_cast<const bf16x8 *>(v_this + d * 64 * BN + v_rd[ks]);
+        const bf16x8 vf = *reinterpret_cast<const bf16x8 *>(v_this + (d_base + d) * 64 * BN + v_rd[ks]);
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb)
           oacc[qb][d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[qb][ks], oacc[qb][d], 0, 0, 0);
@@ -451,14 +456,14 @@ __global__ __launch_bounds__(RB *NPB * 64, ((QB == 1 && D <= 128) || D <= 64) ? 
       const float lt = xor32_sum(l[qb]);
       if (pos < a.S) {
         const long row = ((long)split * a.S + pos) * a.Hq + head;
-        float *op = a.part_o + row * D + 4 * hl;
+        float *op = a.part_o + row * D + 32 * d_base + 4 * hl;
 #pragma unroll
         for (int d = 0; d < DB; ++d)
 #pragma unroll
           for (int g = 0; g < 4; ++g)
             *reinterpret_cast<float4 *>(op + d * 32 + 8 * g) =
                 make_float4(oacc[qb][d][4 * g], oacc[qb][d][4 * g + 1], oacc[qb][d][4 * g + 2], oacc[qb][d][4 * g + 3]);
-        if (hl == 0) {
+        if (hl == 0 && oh == 0) {
           a.part_ml[row * 2] = m[qb];
           a.part_ml[row * 2 + 1] = lt;
         }
@@ -474,9 +479,10 @@ __global__ __launch_bounds__(RB *NPB * 64, ((QB == 1 && D <= 128) || D <= 64) ? 
     const float lt = xor32_sum(l[qb]);
     if (pos < a.S) {
       // positive, finite and non-zero, tested on the bits (NaN fails it)
-      if (hl == 0 && !(__float_as_uint(lt) - 1u < 0x7f7fffffu)) atomicOr(a.err, kDevErrSoftmaxDenominator);
+      if (hl == 0 && oh == 0 && !(__float_as_uint(lt) - 1u < 0x7f7fffffu))
+        atomicOr(a.err, kDevErrSoftmaxDenominator);
       const float inv = 1.0f / lt;
-      float *op = a.out + ((long)pos * a.Hq + head) * D + 4 * hl;
+      float *op = a.out + ((long)pos * a.Hq + head) * D + 32 * d_base + 4 * hl;
 #pragma unroll
       for (int d = 0; d < DB; ++d)
 #pragma unroll
@@ -491,29 +497,39 @@ __global__ __launch_bounds__(RB *NPB * 64, ((QB == 1 && D <= 128) || D <= 64) ? 
 
 namespace {
 
-template <int D, int RB, int NPB, int BN, int QB>
+template <int D, int RB, int NPB, int BN, int QB, int OS>
 hipError_t launch_shape(hipStream_t st, PrefillArgs a) {
   constexpr int WGQ = NPB * QB * 32;
   a.n_qblocks = (a.S + WGQ - 1) / WGQ;
   const long blocks = (long)a.n_qblocks * a.splits * a.Hkv * (a.R / RB);
-  hipLaunchKernelGGL((prefill_kernel<D, RB, NPB, BN, QB>), dim3((unsigned)blocks), dim3(RB * NPB * 64), 0, st,
-                     a);
+  hipLaunchKernelGGL((prefill_kernel<D, RB, NPB, BN, QB, OS>), dim3((unsigned)blocks), dim3(RB * NPB * OS * 64), 0,
+                     st, a);
   return hipGetLastError();
 }
 
-// Four-wave workgroups, 32 queries per wave, 64-key tiles (32 at head_dim
-// 256), two waves per SIMD (one at head_dim 256): four heads of the KV group,
+// Four-wave workgroups (eight with the O split), 32 queries per wave, 64-key
+// tiles (32 at head_dim 256), two waves per SIMD (one at head_dim 256 without
+// the O split): four heads of the KV group,
 // two heads with two blocks, or one head with four blocks. (64 queries per
 // wave halves the LDS fragment reads per
 // MFMA but, at head_dim 128, needs more than 256 VGPRs and measured slower;
 // at head_dim 64 it halves the workgroup count, which a 2048-token prefill
 // cannot afford.)
+template <int D, int BN, int OS>
+hipError_t launch_r(hipStream_t st, const PrefillArgs &a) {
+  if (a.R % 4 == 0) return launch_shape<D, 4, 1, BN, 1, OS>(st, a);
+  if (a.R % 2 == 0) return launch_shape<D, 2, 2, BN, 1, OS>(st, a);
+  return launch_shape<D, 1, 4, BN, 1, OS>(st, a);
+}
+
 template <int D>
 hipError_t launch_d(hipStream_t st, const PrefillArgs &a) {
-  constexpr int BN = D >= 256 ? 32 : 64;  // head_dim 256: 32-key tiles, one wave per SIMD
-  if (a.R % 4 == 0) return launch_shape<D, 4, 1, BN, 1>(st, a);
-  if (a.R % 2 == 0) return launch_shape<D, 2, 2, BN, 1>(st, a);
-  return launch_shape<D, 1, 4, BN, 1>(st, a);
+  constexpr int BN = D >= 256 ? 32 : 64;  // head_dim 256: 32-key tiles
+  if constexpr (D >= 256) {
+    // one wave per SIMD; with O split over two waves, two (for long ranges)
+    if (a.o_split) return launch_r<D, BN, 2>(st, a);
+  }
+  return launch_r<D, BN, 1>(st, a);
 }
 
 }  // namespace
@@ -535,7 +551,8 @@ long prefill_base_workgroups(const PrefillArgs &a, int D) {
 
 // Merges key splits: per (query row, head), M = max m_j, then
 // O = sum_j O_j 2^(m_j - M), L = sum_j l_j 2^(m_j - M), out = O / L. Splits
-// that saw no key of the row (m_j = -inf) contribute nothing. WPR waves share
+// that saw no key of the row (m_j = -inf; their O was never written) are
+// skipped. WPR waves share
 // a row (WPR = 1: four rows per workgroup; WPR = 4: one): lane l holds the
 // row's elements [l * D/64, (l + 1) * D/64), the lanes find M together, and
 // wave w sums splits w, w + WPR, ... in order, reading each split's (m, l)
@@ -583,7 +600,9 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(const PrefillArgs 
 #pragma unroll 8
   for (int j = sub; j < a.splits; j += WPR) {
     const float mj = ml[j * rows * 2], lj = ml[j * rows * 2 + 1];
-    const float g = mj == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(mj - Ms);
+    // a split that saw none of the row's keys wrote no O: skip it (uniform)
+    if (mj == -__builtin_inff()) continue;
+    const float g = __builtin_amdgcn_exp2f(mj - Ms);
     float o[E];
     load_e<E>(po + j * rows * D, o);
 #pragma unroll
