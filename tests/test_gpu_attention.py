@@ -148,6 +148,24 @@ def test_invalid_softmax_denominator_is_reported(gpu):
     gpu.scaled_dot_product_attention_with_cache(q, k, v, cache, gpu.KvAttentionConfig(1, Hq, Hkv, D, True))
 
 
+def test_split_prefill_ignores_stale_partials_of_empty_splits(gpu):
+    """A causal prefill with key splits: the early query blocks' upper splits
+    see no key and write no partial O. A non-causal call of the same size
+    first fills the same workspace with NaN partials. The combine must skip
+    the empty splits rather than scale the stale NaNs by zero."""
+    S, Hq, Hkv, D = 1024, 4, 1, 256  # 32 workgroups: 7 key splits, most empty for early blocks
+    q, k, v, _, _ = layer_inputs(17, 0, S, 0, Hq, Hkv, D)
+    with pytest.raises(gpu.InvalidTensorDataError):
+        gpu.scaled_dot_product_attention_with_cache(np.full_like(q, np.nan), k, v, None,
+                                                    gpu.KvAttentionConfig(S, Hq, Hkv, D, False))
+    got = gpu.scaled_dot_product_attention_with_cache(q, k, v, None, gpu.KvAttentionConfig(S, Hq, Hkv, D, True))
+    ref = o.sdpa_with_cache(q, k, v, None, S, Hq, Hkv, D, True, 0)
+    assert np.all(np.isfinite(got))
+    err = rel_err(got, ref)
+    print(f"[prefill] stale-workspace split case: rel err {err:.2e}", flush=True)
+    assert err <= BF16_TOL
+
+
 def test_batched_decode_matches_per_sequence_oracle(gpu):
     import torch
 
