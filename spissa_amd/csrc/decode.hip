@@ -304,15 +304,15 @@ __global__ __launch_bounds__(256, 4) void decode_split_kernel(const DecodeArgs a
 // Finishes the attention of one (sequence, KV head, head block): the new
 // token's score and value, merged with the partials of every split of the
 // cached keys, then the optional append of the new key and value.
-// Grid: (RB*D / 64, Hkv*HB, B); 1024 threads = 64 consecutive outputs x 16
-// split lanes. Each lane keeps an online (max, sum, output) over its splits
-// with the loads of four splits in flight; the 16 lanes of every output are
-// merged through LDS.
-template <int D, int RB>
+// Grid: (RB*D / OUTS, Hkv*HB, B); 1024 threads = OUTS consecutive outputs x
+// SL split lanes (64 x 16, or 16 x 64 when there are many splits). Each lane
+// keeps an online (max, sum, output) over its splits with the loads of eight
+// splits in flight; the SL lanes of every output are merged through LDS.
+template <int D, int RB, int SL>
 __global__ __launch_bounds__(1024) void decode_combine_kernel(const DecodeArgs a) {
   constexpr int HALF = D / 2;
   constexpr int ENTRY = RB * (D + 2);
-  constexpr int OUTS = 64, SL = 16, UNROLL = 8;  // one load round up to 128 splits
+  constexpr int OUTS = 1024 / SL, UNROLL = 8;  // one load round up to SL * 8 splits
   __shared__ float s_m[SL][OUTS], s_l[SL][OUTS], s_o[SL][OUTS];
   __shared__ float s_dot[RB * D / 64];
   __shared__ float s_new[RB];
@@ -326,7 +326,7 @@ __global__ __launch_bounds__(1024) void decode_combine_kernel(const DecodeArgs a
   const int tid = threadIdx.x;
   const int out = tid & (OUTS - 1);
   const int sl = tid / OUTS;
-  const int e = blockIdx.x * OUTS + out;  // < RB*D: RB*D is a multiple of 64
+  const int e = blockIdx.x * OUTS + out;  // < RB*D: RB*D is a multiple of OUTS
   const int r = e / D;
   const int qh0 = h * a.R + hb * RB;
   const float *knew = a.cur_k + ((long)b * a.Hkv + h) * D;
@@ -446,6 +446,9 @@ namespace {
 // stay resident per CU.
 constexpr int rows_per_group(int RB) { return RB >= 4 ? 2 : 3; }
 
+// Above this many splits the combine gives each output 64 split lanes.
+constexpr int kCombineWideSplits = 128;
+
 template <int D, int RB>
 hipError_t launch_one(hipStream_t st, const DecodeArgs &a) {
   if (a.max_splits > 0) {
@@ -454,8 +457,13 @@ hipError_t launch_one(hipStream_t st, const DecodeArgs &a) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  dim3 cgrid((unsigned)(RB * D / 64), (unsigned)(a.Hkv * a.HB), (unsigned)a.B);
-  hipLaunchKernelGGL((decode_combine_kernel<D, RB>), cgrid, dim3(1024), 0, st, a);
+  if (a.max_splits > kCombineWideSplits) {
+    dim3 cgrid((unsigned)(RB * D / 16), (unsigned)(a.Hkv * a.HB), (unsigned)a.B);
+    hipLaunchKernelGGL((decode_combine_kernel<D, RB, 64>), cgrid, dim3(1024), 0, st, a);
+  } else {
+    dim3 cgrid((unsigned)(RB * D / 64), (unsigned)(a.Hkv * a.HB), (unsigned)a.B);
+    hipLaunchKernelGGL((decode_combine_kernel<D, RB, 16>), cgrid, dim3(1024), 0, st, a);
+  }
   return hipGetLastError();
 }
 
