@@ -483,11 +483,9 @@ bool decode_supported(int D, int R) { return (D == 64 || D == 128 || D == 256) &
 
 int decode_keys_per_split(int D, int RB, long total_rows, int max_keys) {
   const int chunk = 4 * (64 / (D / 8)) * rows_per_group(RB);  // keys of one workgroup iteration
-  static const long target = [] {
-    const char *env = getenv("SPISSA_DECODE_TARGET_WGS");
-    const long v = env ? atol(env) : 0;
-    return v > 0 ? v : 1024L;
-  }();
+  // about 1024 workgroups over the launch (grids of exactly 3 or 4 per CU
+  // measured no faster)
+  constexpr long target = 1024;
   const long per = (total_rows + target - 1) / target;
   long kps = ((per + chunk - 1) / chunk) * chunk;
   if (kps < chunk) kps = chunk;
