@@ -1,4 +1,4 @@
-"""Benchmark of the MI355X attention path at the Llama-3.2-3B shape (BASELINE config 3).
+"""Benchmark of the MI355X attention path at the Llama-3.2-3B shape (BASELINE.json configs[2]).
 
 One step = one decode token through all 28 attention layers at batch 1:
 per layer, RoPE of q/k from the resident table, split-K f32 decode against
@@ -445,7 +445,8 @@ def lm_head_bench(sess, stream, gen, dev, args, time_graph) -> dict:
 # The attention layers of the other BASELINE configs, each measured over
 # `layers` distinct caches (more than the 256 MB last-level cache holds, where
 # the reads are large enough to matter):
-# (name, BASELINE config, layers, Hq, Hkv, d, query rows S, cached rows P, window, llama RoPE)
+# (name, index i of BASELINE.json configs[i], layers, Hq, Hkv, d, query rows S, cached rows P, window,
+#  llama RoPE)
 CONFIG_CASES = [
     ("llama32_1b_decode_512", 0, 16, 32, 8, 64, 1, 512, 0, True),
     ("llama32_1b_prefill_2048", 1, 16, 32, 8, 64, 2048, 0, 0, False),
