@@ -1257,6 +1257,34 @@ static int linear_launch(spissa_session *s, const spissa_linear_weight *w, const
   return SPISSA_OK;
 }
 
+// Several weights applied to the same input (the q, k and v projections):
+// one GEMV launch when all take the GEMV on an aligned input, else one
+// launch each. Results equal those of separate linear_launch calls.
+static int linear_launch_multi(spissa_session *s, const spissa_linear_weight *const *w, const float *d_x,
+                               size_t batch, float *const *d_out, int n) {
+  if (batch == 0) return SPISSA_OK;
+  if (batch > INT32_MAX) return set_err(SPISSA_ERR_SHAPE, "batch %zu too large", batch);
+  if (reinterpret_cast<uintptr_t>(d_x) & 15) {
+    for (int i = 0; i < n; ++i) ST_TRY(linear_launch(s, w[i], d_x, nullptr, batch, d_out[i]));
+    return SPISSA_OK;
+  }
+  LinearArgs a[kMaxLinearSegments];
+  for (int i = 0; i < n; ++i) {
+    a[i] = LinearArgs{};
+    a[i].w = w[i]->data;
+    a[i].x = d_x;
+    a[i].bias = nullptr;
+    a[i].out = d_out[i];
+    a[i].M = (int)batch;
+    a[i].N = (int)w[i]->out_features;
+    a[i].K = (int)w[i]->in_features;
+    a[i].dtype = w[i]->dtype;
+  }
+  HIP_TRY(hipSetDevice(s->device));
+  HIP_TRY(launch_linear_multi(s->stream, a, n));
+  return SPISSA_OK;
+}
+
 extern "C" int spissa_linear(const spissa_linear_weight *w, const float *input, size_t input_len, const float *bias,
                              size_t bias_len, const spissa_linear_config *cfg, float *out, size_t out_len) {
   GUARD_BEGIN
@@ -1458,9 +1486,11 @@ extern "C" int spissa_attention_sublayer_device(spissa_session *s, const spissa_
     xn = r[0];
   }
   float *q = r[1], *k = r[2], *v = r[3], *att = r[4];
-  ST_TRY(linear_launch(s, L->q_weight, xn, nullptr, S, q));
-  ST_TRY(linear_launch(s, L->k_weight, xn, nullptr, S, k));
-  ST_TRY(linear_launch(s, L->v_weight, xn, nullptr, S, v));
+  {
+    const spissa_linear_weight *const wqkv[3] = {L->q_weight, L->k_weight, L->v_weight};
+    float *const oqkv[3] = {q, k, v};
+    ST_TRY(linear_launch_multi(s, wqkv, xn, S, oqkv, 3));
+  }
   if (qk_norm)
     ST_TRY(spissa_gemma_qk_prologue_device(s, L->rope, q, k, S, Hq, Hkv, D, L->d_q_norm, L->d_k_norm, L->eps, pos,
                                            L->q_prescale));

@@ -155,6 +155,16 @@ hipError_t launch_generic(hipStream_t st, const GenericArgs &a);
 // with K % 32 == 0; else kLinearGeneric), and its launch. The vector paths also need 16-byte aligned x and weight rows.
 int linear_path(int dtype, long M, long K);
 hipError_t launch_linear(hipStream_t st, const LinearArgs &a, int path);
+// Projections of one input [M, K] by several weights in one GEMV launch when
+// every segment takes the GEMV path with the same M, K, dtype and x (16-byte
+// aligned); otherwise one launch each.
+constexpr int kMaxLinearSegments = 3;
+struct LinearSegments {
+  LinearArgs seg[kMaxLinearSegments];
+  int blocks[kMaxLinearSegments];  // workgroups of each segment
+  int n;
+};
+hipError_t launch_linear_multi(hipStream_t st, const LinearArgs *segs, int n);
 
 // Greedy token choice: one partial per contiguous range of the logits.
 struct ArgmaxPart {

@@ -97,14 +97,14 @@ constexpr int kGemvRowsPerWave = 2;
 
 }  // namespace
 
-// Grid: ceil(N / (4 * kGemvRowsPerWave)) workgroups of 256 threads. K is a
+// The rows of workgroup `block`: 4 * kGemvRowsPerWave of them. K is a
 // multiple of the chunk width (8 for 16-bit weights, 4 for f32).
 template <typename WT, int NB>
-__global__ __launch_bounds__(256) void linear_gemv_kernel(const LinearArgs a) {
+__device__ __forceinline__ void gemv_rows(const LinearArgs &a, int block) {
   using C = WChunk<WT>;
   constexpr int EPC = C::N, RW = kGemvRowsPerWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int r0 = (blockIdx.x * 4 + wave) * RW;
+  const int r0 = (block * 4 + wave) * RW;
   if (r0 >= a.N) return;  // uniform per wave
   const int nch = a.K / EPC;
   const char *wb = reinterpret_cast<const char *>(a.w);
@@ -165,6 +165,24 @@ __global__ __launch_bounds__(256) void linear_gemv_kernel(const LinearArgs a) {
       for (int tt = 0; tt < NB; ++tt) v = (ii == i && tt == t) ? acc[ii][tt] : v;
     if (r < a.N) a.out[(long)t * a.N + r] = (a.bias ? a.bias[r] : 0.0f) + v;
   }
+}
+
+
+// Grid: ceil(N / (4 * kGemvRowsPerWave)) workgroups of 256 threads.
+template <typename WT, int NB>
+__global__ __launch_bounds__(256) void linear_gemv_kernel(const LinearArgs a) {
+  gemv_rows<WT, NB>(a, blockIdx.x);
+}
+
+// Several projections of the same input in one launch (the q, k and v
+// weights of a layer). Workgroup b belongs to the first segment whose
+// cumulative workgroup count exceeds b; within it, the rows and arithmetic
+// are those of linear_gemv_kernel, so the results are identical.
+template <typename WT, int NB>
+__global__ __launch_bounds__(256) void linear_gemv_multi_kernel(const LinearSegments m) {
+  int b = blockIdx.x, seg = 0;
+  while (seg + 1 < m.n && b >= m.blocks[seg]) b -= m.blocks[seg++];
+  gemv_rows<WT, NB>(seg == 0 ? m.seg[0] : seg == 1 ? m.seg[1] : m.seg[2], b);
 }
 
 namespace {
@@ -480,6 +498,19 @@ hipError_t launch_gemv(hipStream_t st, const LinearArgs &a) {
   return hipGetLastError();
 }
 template <typename WT>
+hipError_t launch_gemv_multi(hipStream_t st, const LinearSegments &m) {
+  long total = 0;
+  for (int i = 0; i < m.n; ++i) total += m.blocks[i];
+  switch (m.seg[0].M) {
+    case 1: hipLaunchKernelGGL((linear_gemv_multi_kernel<WT, 1>), dim3((unsigned)total), dim3(256), 0, st, m); break;
+    case 2: hipLaunchKernelGGL((linear_gemv_multi_kernel<WT, 2>), dim3((unsigned)total), dim3(256), 0, st, m); break;
+    case 3: hipLaunchKernelGGL((linear_gemv_multi_kernel<WT, 3>), dim3((unsigned)total), dim3(256), 0, st, m); break;
+    case 4: hipLaunchKernelGGL((linear_gemv_multi_kernel<WT, 4>), dim3((unsigned)total), dim3(256), 0, st, m); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+template <typename WT>
 hipError_t launch_generic_linear(hipStream_t st, const LinearArgs &a) {
   const long n = (long)a.M * a.N;
   hipLaunchKernelGGL((linear_generic_kernel<WT>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a);
@@ -498,6 +529,32 @@ int linear_path(int dtype, long M, long K) {
   if (dtype == SPISSA_DTYPE_BF16 && M > 4 && K % kBK == 0) return kLinearGemm;
   if (M <= 4 && K % epc == 0) return kLinearGemv;
   return kLinearGeneric;
+}
+
+hipError_t launch_linear_multi(hipStream_t st, const LinearArgs *segs, int n) {
+  if (n < 1 || n > kMaxLinearSegments) return hipErrorInvalidValue;
+  LinearSegments m{};
+  m.n = n;
+  for (int i = 0; i < n; ++i) {
+    const LinearArgs &a = segs[i];
+    // one launch only when every segment takes the GEMV with the same input shape
+    if (a.M != segs[0].M || a.K != segs[0].K || a.dtype != segs[0].dtype || a.x != segs[0].x || a.N <= 0 ||
+        linear_path(a.dtype, a.M, a.K) != kLinearGemv) {
+      for (int j = 0; j < n; ++j) {
+        const hipError_t e = launch_linear(st, segs[j], linear_path(segs[j].dtype, segs[j].M, segs[j].K));
+        if (e != hipSuccess) return e;
+      }
+      return hipSuccess;
+    }
+    m.seg[i] = a;
+    m.blocks[i] = (a.N + 4 * kGemvRowsPerWave - 1) / (4 * kGemvRowsPerWave);
+  }
+  switch (segs[0].dtype) {
+    case SPISSA_DTYPE_F32: return launch_gemv_multi<float>(st, m);
+    case SPISSA_DTYPE_BF16: return launch_gemv_multi<__bf16>(st, m);
+    case SPISSA_DTYPE_F16: return launch_gemv_multi<_Float16>(st, m);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_linear(hipStream_t st, const LinearArgs &a, int path) {
