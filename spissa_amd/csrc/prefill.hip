@@ -120,12 +120,13 @@ struct Geom {
 };
 
 // S^T of one key tile for the wave's QB query blocks over the 16-dim steps
-// [T0, T1): the first step starts from zero (ZERO) or from s (the mask bias),
-// later ones accumulate; kbuf is the K tile in LDS.
-template <int D, int BN, int QB, int T0, int T1, bool ZERO>
+// [T0, T1): the first step starts from the row bias (BIAS: every element of
+// bias[qb] is minus the row's exponent reference) or from s (a masked tile's
+// start, already in s); later ones accumulate; kbuf is the K tile in LDS.
+template <int D, int BN, int QB, int T0, int T1, bool BIAS>
 __device__ __forceinline__ void score_tile(f32x16 (&s)[QB][BN / 32], const char *kbuf,
                                            const unsigned (&k_rd)[D / 16],
-                                           const bf16x8 (&qf)[QB][D / 16]) {
+                                           const bf16x8 (&qf)[QB][D / 16], const f32x16 (&bias)[QB]) {
   constexpr int KB = BN / 32;
 #pragma unroll
   for (int tt = T0; tt < T1; ++tt)
@@ -134,10 +135,20 @@ __device__ __forceinline__ void score_tile(f32x16 (&s)[QB][BN / 32], const char 
       const bf16x8 kf = *reinterpret_cast<const bf16x8 *>(kbuf + kb * 64 * D + k_rd[tt]);
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
-        const f32x16 acc = (ZERO && tt == T0) ? f32x16{} : s[qb][kb];
+        const f32x16 acc = (BIAS && tt == T0) ? bias[qb] : s[qb][kb];
         s[qb][kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[qb][tt], acc, 0, 0, 0);
       }
     }
+}
+
+// Sum of the eight bf16 probabilities of p (v_dot2c_f32_bf16 against 1.0 pairs).
+__device__ __forceinline__ float sum_bf16x8(const bf16x8 p) {
+  typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+  const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+  float s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p, p, 0, 1), one, 0.0f, false);
+  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p, p, 2, 3), one, s, false);
+  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p, p, 4, 5), one, s, false);
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p, p, 6, 7), one, s, false);
 }
 
 }  // namespace
@@ -206,6 +217,9 @@ prefill_kernel(const PrefillArgs a) {
   }
 
   // Q^T (B operand): lane holds query lq of block qb, dims 16t + 8hl + [0,8).
+  // Q carries the softmax scale times log2(e), so the scores come out of the
+  // MFMAs in the log2 domain.
+  const float c = a.qk_scale_log2;
   bf16x8 qf[QB][DT];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
@@ -216,8 +230,8 @@ prefill_kernel(const PrefillArgs a) {
       const float4 x0 = *reinterpret_cast<const float4 *>(qp + 16 * t);
       const float4 x1 = *reinterpret_cast<const float4 *>(qp + 16 * t + 4);
       bf16x8 v;
-      v[0] = (bf16)x0.x; v[1] = (bf16)x0.y; v[2] = (bf16)x0.z; v[3] = (bf16)x0.w;
-      v[4] = (bf16)x1.x; v[5] = (bf16)x1.y; v[6] = (bf16)x1.z; v[7] = (bf16)x1.w;
+      v[0] = (bf16)(x0.x * c); v[1] = (bf16)(x0.y * c); v[2] = (bf16)(x0.z * c); v[3] = (bf16)(x0.w * c);
+      v[4] = (bf16)(x1.x * c); v[5] = (bf16)(x1.y * c); v[6] = (bf16)(x1.z * c); v[7] = (bf16)(x1.w * c);
       qf[qb][t] = v;
     }
   }
@@ -289,7 +303,6 @@ prefill_kernel(const PrefillArgs a) {
   }
   const int wave_min_q = a.P + wp0;
   const int wave_max_q = a.P + min(wp0 + WQ - 1, a.S - 1);
-  const float c = a.qk_scale_log2;
 
   // Whether tile t needs a mask (uniform): the causal diagonal, the window's
   // lower edge, or keys past the end.
@@ -298,10 +311,16 @@ prefill_kernel(const PrefillArgs a) {
     return (a.causal && kt0 + BN - 1 > wave_min_q) || (a.window > 0 && kt0 + a.window <= wave_max_q) ||
            (kt0 + BN > key_total);
   };
+  // Exponent reference per row: exponentials of a tile are taken against ms
+  // (m, or 0 while m = -inf); m rises only by more than kRescaleSlack. The
+  // score MFMAs start from bias = -ms, so a score accumulator holds
+  // (scaled score - ms) and its exponential needs no subtraction.
+  float ms[QB];
+  f32x16 bias[QB];
   // Masking: the score accumulators of a masked tile start at -inf for the
-  // keys a row does not see (0 elsewhere), so the MFMAs produce -inf there
+  // keys a row does not see (-ms elsewhere), so the MFMAs produce -inf there
   // and the maxima and exponentials need no selects; unmasked tiles start
-  // from an inline zero. Score element i of block kb is key
+  // from the bias registers. Score element i of block kb is key
   // kb*32 + 8(i/4) + 4hl + i%4 of its tile. (Keys beyond the last one are zero
   // padding, so -inf + finite stays -inf.) This issues the first 16-dim step
   // of S(t); score_tile<..., 1, DT, false> adds the rest.
@@ -316,15 +335,15 @@ prefill_kernel(const PrefillArgs a) {
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             const int kk = kb * 32 + 8 * (i >> 2) + (i & 3);
-            s[qb][kb][i] = (kk < lo || kk > hi) ? NEG_INF : 0.0f;
+            s[qb][kb][i] = (kk < lo || kk > hi) ? NEG_INF : -ms[qb];
           }
       }
-      score_tile<D, BN, QB, 0, 1, false>(s, kbuf, k_rd, qf);
+      score_tile<D, BN, QB, 0, 1, false>(s, kbuf, k_rd, qf, bias);
     } else {
-      score_tile<D, BN, QB, 0, 1, true>(s, kbuf, k_rd, qf);
+      score_tile<D, BN, QB, 0, 1, true>(s, kbuf, k_rd, qf, bias);
     }
   };
-  // Row maxima of a score tile (log2 domain).
+  // Row maxima of a score tile (log2 domain, the reference added back).
   auto row_max = [&](const f32x16 (&s)[QB][KB], float (&mx)[QB]) {
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
@@ -333,13 +352,9 @@ prefill_kernel(const PrefillArgs a) {
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) v = vmax(v, s[qb][kb][i]);
-      mx[qb] = xor32_max(v) * c;
+      mx[qb] = xor32_max(v) + ms[qb];
     }
   };
-
-  // Exponent reference per row: exponentials of a tile are taken against ms
-  // (m, or 0 while m = -inf); m rises only by more than kRescaleSlack.
-  float ms[QB];
 
   // One pipelined step on tile t (scores in `cur`, exponent reference ms
   // already covering tile t, O and l already scaled to it):
@@ -369,19 +384,16 @@ prefill_kernel(const PrefillArgs a) {
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         bf16x8 p;
-        float pv[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          pv[j] = fast_exp2(fmaf(cur[qb][ks >> 1][8 * (ks & 1) + j], c, -ms[qb]));
-          p[j] = (bf16)pv[j];
-        }
-        // pairwise: a short dependency chain instead of 32 serial adds
-        const float s8 = ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
+        for (int j = 0; j < 8; ++j) p[j] = (bf16)fast_exp2(cur[qb][ks >> 1][8 * (ks & 1) + j]);
+        // The row sum adds the bf16 probabilities the PV MFMAs use, one chain
+        // per 16-key step.
+        const float s8 = sum_bf16x8(p);
         psum[qb] = ks == 0 ? s8 : psum[qb] + s8;
         pf[qb][ks] = p;
       }
     }
-    score_tile<D, BN, QB, 1, DT, false>(nxt, k_next, k_rd, qf);
+    score_tile<D, BN, QB, 1, DT, false>(nxt, k_next, k_rd, qf, bias);
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) l[qb] += psum[qb];
 
@@ -396,7 +408,7 @@ prefill_kernel(const PrefillArgs a) {
           oacc[qb][d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[qb][ks], oacc[qb][d], 0, 0, 0);
       }
     const bool has_next = t + 1 < t_end;
-    float mx[QB], alpha[QB];
+    float mx[QB], alpha[QB], shift[QB];
     bool raise[QB];
     row_max(nxt, mx);
 #pragma unroll
@@ -405,6 +417,7 @@ prefill_kernel(const PrefillArgs a) {
       const float mnew = raise[qb] ? mx[qb] : m[qb];
       const float msn = mnew == NEG_INF ? 0.0f : mnew;
       alpha[qb] = fast_exp2(m[qb] - msn);
+      shift[qb] = msn - ms[qb];  // 0 unless this row's reference rises
       l[qb] *= alpha[qb];
       m[qb] = mnew;
       ms[qb] = msn;
@@ -419,6 +432,13 @@ prefill_kernel(const PrefillArgs a) {
         for (int d = 0; d < DB; ++d)
 #pragma unroll
           for (int i = 0; i < 16; ++i) oacc[qb][d][i] *= alpha[qb];
+        // S(t+1) was biased by the old reference
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) nxt[qb][kb][i] -= shift[qb];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) bias[qb][i] = -ms[qb];
       }
     wait_copies();
     __syncthreads();
@@ -431,8 +451,14 @@ prefill_kernel(const PrefillArgs a) {
   if (t_begin + 1 < t_end) copy_k(t_begin + 1, k_lds1);
   wait_copies();
   __syncthreads();
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    ms[qb] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) bias[qb][i] = 0.0f;
+  }
   score_first(sa, k_lds0, t_begin);
-  score_tile<D, BN, QB, 1, DT, false>(sa, k_lds0, k_rd, qf);
+  score_tile<D, BN, QB, 1, DT, false>(sa, k_lds0, k_rd, qf, bias);
   {
     float mx[QB];
     row_max(sa, mx);
@@ -440,6 +466,12 @@ prefill_kernel(const PrefillArgs a) {
     for (int qb = 0; qb < QB; ++qb) {
       m[qb] = mx[qb];
       ms[qb] = mx[qb] == NEG_INF ? 0.0f : mx[qb];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sa[qb][kb][i] -= ms[qb];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) bias[qb][i] = -ms[qb];
     }
   }
   __syncthreads();  // every wave is done with K(t0) before K(t0+2) lands in its buffer
