@@ -30,24 +30,28 @@
 // are in flight while
 //   part A: the exponentials of tile t run on the VALU next to the MFMAs of
 //           S(t+1) = K(t+1) Q^T;
-//   part B: O^T += V(t)^T P(t)^T runs on the MFMAs next to the row maxima of
-//           tile t+1, which fix the exponent reference of step t+1;
-// then the (rare) rescale of O and one barrier. Both parts are one basic
-// block, so the compiler interleaves them freely.
-// Masks. The score accumulators of a masked tile (causal diagonal, window
-// edge, keys past the end) start at -inf for the hidden keys instead of 0,
-// so the MFMAs yield -inf there and the maxima and exponentials need no
-// per-element selects; unmasked tiles start from an inline zero.
+//   part B: O^T += V(t)^T P(t)^T runs on the MFMAs (at head_dim 64 and 256
+//           next to the row maxima of tile t+1, which fix the exponent
+//           reference of step t+1);
+// then the (rare) rescale of O and one barrier. The compiler interleaves the
+// VALU and MFMA work of each part freely.
+// Scores. Q is rounded to bf16 after scaling by softmax scale * log2(e), and
+// the score MFMAs start from minus the row's exponent reference, so the
+// accumulators hold (scaled score - reference) and feed the exponentials
+// directly. Masked tiles (causal diagonal, window edge, keys past the end)
+// start at -inf for the hidden keys instead, so the MFMAs yield -inf there
+// and the maxima and exponentials need no per-element selects.
 // Tiles are unpadded; the 16-byte chunks of each row are XOR-swizzled within
 // the row by swz(row), chosen so that the 8 consecutive rows one LDS read
 // serves together (same chunk index) hit 8 distinct 16-byte bank groups:
 //   K tile   [BN keys][D]: chunk c of key row r at byte r*2D  + 16*(c ^ swz(r))
 //   V^T tile [D][BN keys]: chunk c of dim row d at byte d*2BN + 16*(c ^ swz(d))
-// Softmax. The exponent reference m of a row is raised only when the row
-// maximum exceeds it by more than 8 (log2 domain), so exponentials stay
-// below 256 and the O accumulators are rescaled a handful of times per
-// row instead of on most tiles; O and the sum share m, so O / sum is exact
-// softmax arithmetic.
+// Softmax. The exponent reference m of a row is raised rarely: at head_dim
+// 64 and 256 when the next tile's row maximum exceeds it by more than 8
+// (log2 domain); at head_dim 128 only when a tile's probabilities sum past
+// 2^16 (or the row has seen no key yet), which drops the per-tile row
+// maximum. O and the sum share m, so O / sum is exact softmax arithmetic.
+// Row sums add the bf16 probabilities that the PV MFMAs use.
 // This file is compiled with MFMA results in VGPRs (-amdgpu-mfma-vgpr-form):
 // the score accumulators feed VALU code directly instead of round-tripping
 // through AGPRs.
@@ -64,8 +68,13 @@ typedef __attribute__((ext_vector_type(16))) float f32x16;
 typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr float NEG_INF = -__builtin_inff();
-// Largest growth of a row maximum (log2 domain) absorbed without rescaling.
+// Eager raising (head_dim 64 and 256): the largest growth of a row maximum
+// (log2 domain) absorbed without rescaling, checked on every tile.
 constexpr float kRescaleSlack = 8.0f;
+// Lazy raising (head_dim 128): a lane's sum of one tile's probabilities above
+// which its row's exponent reference is raised (the probabilities then stay
+// far from f32 and bf16 overflow, and O keeps full relative precision).
+constexpr float kRaiseSum = 65536.0f;
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -166,6 +175,10 @@ prefill_kernel(const PrefillArgs a) {
   constexpr int WQ = QB * 32;  // queries per wave
   constexpr int WGQ = NPB * WQ;
   using G = Geom<D, BN, NW>;
+  // Exponent reference raised lazily (from the tile's probability sums) or
+  // eagerly (from every next tile's row maxima): lazily measured 2-3% faster
+  // at head_dim 128, eagerly 4-5% faster at 64 and 256.
+  constexpr bool LAZY = D == 128;
   constexpr int DT = G::DT, KB = G::KB, KS = G::KS, DB = G::DB / OS;  // DB: output blocks of this wave
 
   // Four separate LDS objects (not one array): the compiler then knows that
@@ -312,7 +325,8 @@ prefill_kernel(const PrefillArgs a) {
            (kt0 + BN > key_total);
   };
   // Exponent reference per row: exponentials of a tile are taken against ms
-  // (m, or 0 while m = -inf); m rises only by more than kRescaleSlack. The
+  // (m, or 0 while m = -inf); m rises by more than kRescaleSlack (eager) or
+  // when a tile's probabilities sum past kRaiseSum (lazy). The
   // score MFMAs start from bias = -ms, so a score accumulator holds
   // (scaled score - ms) and its exponential needs no subtraction.
   float ms[QB];
@@ -394,8 +408,58 @@ prefill_kernel(const PrefillArgs a) {
       }
     }
     score_tile<D, BN, QB, 1, DT, false>(nxt, k_next, k_rd, qf, bias);
+
+    if constexpr (LAZY) {
+    // The exponent reference is raised lazily: only a row whose probabilities
+    // grew large (a lane's sum above 2^16, i.e. scores well above the
+    // reference) or that has seen no key yet takes the exact maximum of tile
+    // t, rescales O and its sum, recomputes the tile's probabilities and
+    // shifts the bias of S(t+1). No per-tile row maximum is needed otherwise.
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const bool hot = (psum[qb] > kRaiseSum) | (m[qb] == NEG_INF);
+      if (__ballot(hot)) {
+        float v = cur[qb][0][0];
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) v = vmax(v, cur[qb][kb][i]);
+        const float mx = xor32_max(v) + ms[qb];  // tile t's maximum (log2 domain)
+        const float mnew = mx > m[qb] ? mx : m[qb];
+        const float msn = mnew == NEG_INF ? 0.0f : mnew;
+        const float shift = msn - ms[qb];
+        const float alpha = fast_exp2(-shift);
+        l[qb] *= alpha;
+#pragma unroll
+        for (int d = 0; d < DB; ++d)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) oacc[qb][d][i] *= alpha;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          bf16x8 pp;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) pp[j] = (bf16)fast_exp2(cur[qb][ks >> 1][8 * (ks & 1) + j] - shift);
+          const float s8 = sum_bf16x8(pp);
+          psum[qb] = ks == 0 ? s8 : psum[qb] + s8;
+          pf[qb][ks] = pp;
+        }
+        // S(t+1) was biased by the old reference
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) nxt[qb][kb][i] -= shift;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) bias[qb][i] = -msn;
+        m[qb] = mnew;
+        ms[qb] = msn;
+      }
+      l[qb] += psum[qb];
+    }
+
+    } else {
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) l[qb] += psum[qb];
+    }
 
     // Part B.
 #pragma unroll
@@ -407,6 +471,7 @@ prefill_kernel(const PrefillArgs a) {
         for (int qb = 0; qb < QB; ++qb)
           oacc[qb][d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[qb][ks], oacc[qb][d], 0, 0, 0);
       }
+    if constexpr (!LAZY) {
     const bool has_next = t + 1 < t_end;
     float mx[QB], alpha[QB], shift[QB];
     bool raise[QB];
@@ -440,6 +505,7 @@ prefill_kernel(const PrefillArgs a) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) bias[qb][i] = -ms[qb];
       }
+    }
     wait_copies();
     __syncthreads();
   };
