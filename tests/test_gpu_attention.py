@@ -71,6 +71,10 @@ def test_decode_generic_head_dims(gpu, D):
     ("33 tokens", 33, 0, 6, 2, 128, 0),
     ("R=8", 70, 10, 32, 4, 64, 0),
     ("R=1 MHA", 100, 3, 4, 4, 128, 0),
+    # head_dim 128 with a window: rows whose first key tile lies wholly
+    # outside their window have seen no key after the first tile
+    ("llama-3B shape local W64", 300, 0, 24, 8, 128, 64),
+    ("llama-3B shape chunk local W100", 96, 500, 24, 8, 128, 100),
 ])
 def test_prefill_bf16_parity(gpu, name, S, P, Hq, Hkv, D, window):
     print(f"[case] prefill {name} S={S} P={P} Hq={Hq} Hkv={Hkv} D={D} W={window}", flush=True)
@@ -133,6 +137,37 @@ def test_reference_kats_through_the_gpu(gpu):
     out = gpu.scaled_dot_product_attention(q, q.copy(), f(10.0, 0.0, 0.0, 20.0), 2, 1, 2, True)
     np.testing.assert_allclose(out[:2], [10.0, 0.0], atol=1e-6)
     assert 3.0 < out[2] < 3.4 and 13.0 < out[3] < 13.7
+
+
+@pytest.mark.parametrize("D,Hq,Hkv", [(64, 8, 2), (128, 6, 2), (256, 4, 1)])
+def test_prefill_reference_rises_across_tiles(gpu, D, Hq, Hkv):
+    """Scores that jump by about 140 (log2 units) after the first 64 keys: the
+    exponent reference taken from the first key tile is far too low for the
+    rest, so the kernel must raise it (lazily from the probability sums at
+    head_dim 128, from the next tile's row maxima otherwise); without the
+    raise the later probabilities would overflow to inf (2^140). Compared
+    with the oracle on the same inputs."""
+    S = 320
+    print(f"[case] prefill reference rise D={D} Hq={Hq} Hkv={Hkv} S={S}", flush=True)
+    q, k, v, _, _ = layer_inputs(17, D, S, 0, Hq, Hkv, D)
+    # a common component of every query row along dim 0, and keys 0..63
+    # pointing against it: their scores sit ~140 log2 units below the rest
+    amp = float(np.sqrt(140.0 / 1.4426950408889634 * np.sqrt(D)))
+    q = q.reshape(S, Hq, D)
+    q[:, :, 0] += amp
+    k = k.reshape(S, Hkv, D)
+    k[:64, :, 0] -= amp
+    k[64:, :, 0] = 0.0  # the later keys' scores stay moderate (no amp x k term)
+    q, k = q.ravel().copy(), k.ravel().copy()
+    ref = o.sdpa_with_cache(q, k, v, None, S, Hq, Hkv, D, True, 0)
+    got = gpu.scaled_dot_product_attention_with_cache(q, k, v, None, gpu.KvAttentionConfig(S, Hq, Hkv, D, True))
+    assert np.all(np.isfinite(got))
+    # Rows 64.. see the later keys, whose scores are moderate, so bf16 scores
+    # are accurate there. (Rows 0-63 see only the shifted keys, whose large
+    # raw scores carry bf16 rounding errors of several units; they never need
+    # a raise.)
+    lo = 64 * Hq * D
+    assert rel_err(got[lo:], ref[lo:]) <= BF16_TOL
 
 
 def test_invalid_softmax_denominator_is_reported(gpu):
