@@ -221,6 +221,37 @@ int spissa_decode_step_device(spissa_session *s, const spissa_rope_table *table,
                               const float *d_q, const float *d_k, const float *d_v,
                               spissa_kv_cache *const *caches, size_t batch,
                               const spissa_kv_attention_config *cfg, float *d_out);
+/* Launch geometry of one attention call as the call itself computes it, on
+ * the host, with no device work. No reference counterpart: it lets a caller
+ * size workspaces before capturing a graph, and lets tests check the host
+ * arithmetic against the kernels' index ranges without a GPU. Caches are
+ * assumed under 4 GiB per buffer (the decode kernel's limit). */
+typedef enum {
+    SPISSA_KERNEL_DECODE = 0,       /* split-K f32 decode (query_len == 1) */
+    SPISSA_KERNEL_PREFILL_BF16 = 1, /* bf16-MFMA prefill (query_len > 1) */
+    SPISSA_KERNEL_GENERIC = 2       /* f32 SIMT kernel (other head dims, f32 prefill) */
+} spissa_kernel_path;
+typedef struct {
+    int path;               /* spissa_kernel_path */
+    int heads_per_block;    /* decode: query heads sharing one K/V read */
+    int head_blocks;        /* decode: head blocks per KV head */
+    int keys_per_split;     /* decode: cached keys per split workgroup */
+    int splits;             /* decode: splits of the longest sequence; prefill: key splits (1: none) */
+    int tiles_per_split;    /* prefill with key splits: key tiles per split */
+    int tile_keys;          /* prefill: keys per tile */
+    int workgroup_queries;  /* prefill: queries per workgroup */
+    int o_split;            /* prefill: head_dim-256 output split over two waves */
+    long max_tiles;         /* prefill: most key tiles one unsplit workgroup visits */
+    size_t workgroups;      /* attention kernel grid (decode: its first launch of <= 16 sequences) */
+    size_t partial_bytes;   /* decode: split partials of the largest launch; prefill: key-split partials */
+    size_t stage_bytes;     /* prefill: bf16 staging of the chunk's K and V^T */
+} spissa_attention_plan;
+/* past_lens[b]: cached tokens of sequence b, batch >= 1 (batch > 1 only with
+ * query_len == 1); compute_units <= 0 means 256; prefill_precision as
+ * spissa_session_set_prefill_precision. */
+int spissa_plan_attention(const spissa_kv_attention_config *cfg, const size_t *past_lens, size_t batch,
+                          int compute_units, int prefill_precision, spissa_attention_plan *out);
+
 /* ops.rs:237-291 scaled_dot_product_attention (cacheless MHA, f32). */
 int spissa_scaled_dot_product_attention(const float *q, size_t q_len, const float *k,
                                         size_t k_len, const float *v, size_t v_len,

@@ -10,6 +10,7 @@ checker or the timed CPU baseline. spissa_amd never imports it.
 from __future__ import annotations
 
 import ctypes as C
+import os
 import subprocess
 from pathlib import Path
 from typing import Optional
@@ -57,12 +58,18 @@ def build() -> Path:
 
 
 def load() -> C.CDLL:
+    """Loads the oracle library; SPISSA_ORACLE_LIB names another build of the
+    same sources (the Makefile's `asan` target, for a sanitizer run)."""
     global _lib
     if _lib is not None:
         return _lib
-    if not LIB_PATH.exists():
-        build()
-    lib = C.CDLL(str(LIB_PATH))
+    alt = os.environ.get("SPISSA_ORACLE_LIB")
+    if alt:
+        lib = C.CDLL(alt)
+    else:
+        if not LIB_PATH.exists():
+            build()
+        lib = C.CDLL(str(LIB_PATH))
     sig = {
         "or_last_error": (C.c_char_p, []),
         "or_gpt_neox_rotary_dim": (C.c_int, [_sz, C.c_float, C.POINTER(_sz)]),

@@ -77,6 +77,22 @@ class AttnConfigC(C.Structure):
     ]
 
 
+KERNEL_DECODE = 0
+KERNEL_PREFILL_BF16 = 1
+KERNEL_GENERIC = 2
+
+
+class AttentionPlanC(C.Structure):
+    """spissa_attention_plan: the launch geometry of one attention call."""
+
+    _fields_ = [
+        ("path", C.c_int), ("heads_per_block", C.c_int), ("head_blocks", C.c_int),
+        ("keys_per_split", C.c_int), ("splits", C.c_int), ("tiles_per_split", C.c_int),
+        ("tile_keys", C.c_int), ("workgroup_queries", C.c_int), ("o_split", C.c_int),
+        ("max_tiles", C.c_long), ("workgroups", c_size), ("partial_bytes", c_size), ("stage_bytes", c_size),
+    ]
+
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "spissa_last_error": (C.c_char_p, []),
@@ -147,6 +163,9 @@ SIGNATURES = {
         C.c_int,
         [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, C.POINTER(c_void_p), c_size,
          C.POINTER(AttnConfigC), c_void_p]),
+    "spissa_plan_attention": (
+        C.c_int,
+        [C.POINTER(AttnConfigC), C.POINTER(c_size), c_size, C.c_int, C.c_int, C.POINTER(AttentionPlanC)]),
     "spissa_scaled_dot_product_attention": (
         C.c_int,
         [c_float_p, c_size, c_float_p, c_size, c_float_p, c_size, c_size, c_size, c_size, C.c_int,

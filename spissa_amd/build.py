@@ -44,6 +44,10 @@ EXTRA = {
     "prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
+# The link line: flags before the objects, libraries after them.
+LINK = [f"--offload-arch={ARCH}", "-shared", "-fPIC"]
+LINK_LIBS = ["-lpthread"]
+
 
 def _compile(src: Path, verbose: bool) -> Path:
     obj = OBJ / (src.stem + ".o")
@@ -72,8 +76,7 @@ def build(verbose: bool = False) -> Path:
     with cf.ThreadPoolExecutor(workers) as ex:
         objs = list(ex.map(lambda s: _compile(s, verbose), sources))
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
-           "-lpthread"]
+    cmd = [HIPCC, *LINK, "-o", str(tmp), *map(str, objs), *LINK_LIBS]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

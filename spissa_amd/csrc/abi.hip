@@ -45,6 +45,12 @@ static int set_err(int code, const char *fmt, ...) {
                      __FILE__, __LINE__);                                                   \
   } while (0)
 
+#define ST_TRY(expr)        \
+  do {                      \
+    int st_ = (expr);       \
+    if (st_) return st_;    \
+  } while (0)
+
 #define GUARD_BEGIN try {
 #define GUARD_END                                                                 \
   }                                                                               \
@@ -67,6 +73,7 @@ struct DevBuf {
   void *p = nullptr;
   size_t bytes = 0;
 };
+
 
 struct spissa_session {
   int device = 0;
@@ -110,8 +117,23 @@ struct spissa_rope_table {
   float *cos = nullptr, *sin = nullptr;  // [max_positions, half]
 };
 
-static int ensure_buf(spissa_session *s, DevBuf &b, size_t bytes, bool zero) {
+// Device memory cannot be allocated while `stream` is being captured into a
+// HIP graph; a call that would allocate then fails with this message instead
+// of a generic device error.
+static int no_capture(hipStream_t stream, const char *what, size_t bytes) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  HIP_TRY(hipStreamIsCapturing(stream, &cs));
+  if (cs != hipStreamCaptureStatusNone)
+    return set_err(SPISSA_ERR_ARGUMENT,
+                   "%s would allocate %zu bytes while the session stream is being captured into a graph; run the "
+                   "same call once before capturing",
+                   what, bytes);
+  return SPISSA_OK;
+}
+
+static int ensure_buf(spissa_session *s, DevBuf &b, size_t bytes) {
   if (bytes <= b.bytes) return SPISSA_OK;
+  ST_TRY(no_capture(s->stream, "the session workspace", bytes));
   size_t want = std::max(bytes, b.bytes + b.bytes / 2);
   want = (want + 4095) & ~(size_t)4095;
   HIP_TRY(hipSetDevice(s->device));
@@ -119,10 +141,6 @@ static int ensure_buf(spissa_session *s, DevBuf &b, size_t bytes, bool zero) {
   HIP_TRY(hipMalloc(&p, want));
   if (b.p) s->retired.push_back(b.p);
   b.p = p;
-  if (zero) {
-    HIP_TRY(hipMemsetAsync(b.p, 0, want, s->stream));
-    HIP_TRY(hipStreamSynchronize(s->stream));
-  }
   b.bytes = want;
   return SPISSA_OK;
 }
@@ -242,7 +260,7 @@ extern "C" int spissa_session_set_prefill_precision(spissa_session *s, int preci
 static int io_regions(spissa_session *s, std::initializer_list<size_t> sizes, float **out) {
   size_t total = 0;
   for (size_t n : sizes) total += (n + 63) & ~(size_t)63;
-  int st = ensure_buf(s, s->io, std::max<size_t>(total, 64) * sizeof(float), false);
+  int st = ensure_buf(s, s->io, std::max<size_t>(total, 64) * sizeof(float));
   if (st) return st;
   float *p = (float *)s->io.p;
   int i = 0;
@@ -267,12 +285,6 @@ static int sync_stream(spissa_session *s) {
   HIP_TRY(hipStreamSynchronize(s->stream));
   return SPISSA_OK;
 }
-
-#define ST_TRY(expr)        \
-  do {                      \
-    int st_ = (expr);       \
-    if (st_) return st_;    \
-  } while (0)
 
 // ------------------------------------------------------------------------
 // KV cache (rotary.rs:195-318)
@@ -375,6 +387,7 @@ static int ensure_shadow(spissa_kv_cache *c, hipStream_t st) {
   if (c->kb) return SPISSA_OK;
   const size_t cap = (c->max_seq_len + 63) & ~(size_t)63;
   const size_t elems = cap * c->width();
+  ST_TRY(no_capture(st, "the cache's bf16 prefill shadow", 2 * elems * sizeof(bf16)));
   HIP_TRY(hipSetDevice(c->session->device));
   HIP_TRY(hipMalloc(&c->kb, elems * sizeof(bf16)));
   hipError_t e = hipMalloc(&c->vt, elems * sizeof(bf16));
@@ -888,33 +901,71 @@ static int pick_rb(int R) {
   return 1;
 }
 
+// Launch plan of one split-K decode launch over B <= kMaxDecodeBatch
+// sequences with past[b] cached tokens each.
+struct DecodePlan {
+  int RB = 1, HB = 1;    // query heads per block, head blocks per KV head
+  int kps = 0;           // cached keys per split
+  int max_splits = 0;    // splits of the longest sequence
+  size_t workgroups = 0; // split-kernel grid
+  size_t partial_bytes = 0;
+};
+
+// partial_cap: bytes available for the partials (0: unbounded). Returns false
+// when even one split per (sequence, KV head, head block) does not fit.
+static bool plan_decode(int D, int Hq, int Hkv, size_t window, const int *past, int B, size_t partial_cap,
+                        DecodePlan *p) {
+  const int R = Hq / Hkv;
+  p->RB = pick_rb(R);
+  p->HB = R / p->RB;
+  long total_rows = 0;
+  int max_keys = 0;
+  for (int b = 0; b < B; ++b) {
+    const int P = past[b];
+    const int kstart = window > 0 ? std::max(0, P + 1 - (int)window) : 0;
+    const int cached = P - kstart;  // visible cached keys; the new token is handled apart
+    max_keys = std::max(max_keys, cached);
+    total_rows += (long)cached * Hkv * p->HB;
+  }
+  const size_t groups = (size_t)B * Hkv * p->HB;
+  const size_t entry = (size_t)p->RB * (D + 2) * sizeof(float);
+  int split_cap = kMaxDecodeSplits;
+  if (partial_cap) {
+    const size_t fit = partial_cap / (groups * entry);
+    if (fit < 1) return false;
+    split_cap = (int)std::min<size_t>(fit, kMaxDecodeSplits);
+  }
+  p->kps = decode_keys_per_split(D, p->RB, total_rows, std::max(1, max_keys), split_cap);
+  p->max_splits = (max_keys + p->kps - 1) / p->kps;
+  p->workgroups = groups * p->max_splits;
+  p->partial_bytes = groups * std::max(1, p->max_splits) * entry;
+  return true;
+}
+
 // Split-K decode over `batch` sequences (one new token each). Optionally fuses
 // the RoPE of q/k from `table` (rotate-half over the whole head) and the
 // append of the new key and value to each cache; the caller has validated
-// capacity when `append` is set.
+// capacity when `append` is set. The partials go to the session workspace,
+// or, with `fixed` set, to the fixed_bytes at `fixed` (splits are coarsened
+// to fit; the caller has checked that one split per group fits).
 static int run_decode(spissa_session *s, const float *d_q, const float *d_k, const float *d_v,
                       const spissa_kv_cache *const *caches, size_t batch, const spissa_kv_attention_config *c,
-                      float *d_out, const spissa_rope_table *table, bool append) {
+                      float *d_out, const spissa_rope_table *table, bool append, float *fixed = nullptr,
+                      size_t fixed_bytes = 0) {
   const int D = (int)c->head_dim, Hq = (int)c->num_heads, Hkv = (int)c->kv_heads;
   const int R = Hq / Hkv;
-  const int RB = pick_rb(R);
-  const int HB = R / RB;
   for (size_t b0 = 0; b0 < batch; b0 += kMaxDecodeBatch) {
     const int B = (int)std::min<size_t>(kMaxDecodeBatch, batch - b0);
     DecodeArgs a;
     memset(&a, 0, sizeof a);
-    long total_rows = 0;
-    int max_keys = 0;
+    int past[kMaxDecodeBatch];
     for (int b = 0; b < B; ++b) {
       const spissa_kv_cache *cb = caches ? caches[b0 + b] : nullptr;
       const int P = cb ? (int)cb->len : 0;
+      past[b] = P;
       a.seq[b].k = cb ? cb->keys : nullptr;
       a.seq[b].v = cb ? cb->values : nullptr;
       a.seq[b].past = P;
-      const int kstart = c->window > 0 ? std::max(0, P + 1 - (int)c->window) : 0;
-      const int cached = P - kstart;  // visible cached keys; the new token is handled apart
-      max_keys = std::max(max_keys, cached);
-      total_rows += (long)cached * Hkv * HB;
       if (append) {
         a.app_k[b] = cb->keys + (size_t)P * cb->width();
         a.app_v[b] = cb->values + (size_t)P * cb->width();
@@ -923,15 +974,17 @@ static int run_decode(spissa_session *s, const float *d_q, const float *d_k, con
         a.app_cap[b] = (long)cb->shadow_cap;
       }
     }
-    const int kps = decode_keys_per_split(D, RB, total_rows, std::max(1, max_keys));
-    const int max_splits = (max_keys + kps - 1) / kps;
-    const size_t groups = (size_t)B * Hkv * HB;
-    ST_TRY(ensure_buf(s, s->partial, groups * std::max(1, max_splits) * RB * (D + 2) * sizeof(float), false));
+    DecodePlan plan;
+    if (!plan_decode(D, Hq, Hkv, c->window, past, B, fixed ? fixed_bytes : 0, &plan))
+      return set_err(SPISSA_ERR_SHAPE, "decode partials of %d sequences x %d heads exceed %zu bytes", B, Hq,
+                     fixed_bytes);
+    const int RB = plan.RB, HB = plan.HB, kps = plan.kps, max_splits = plan.max_splits;
+    if (!fixed) ST_TRY(ensure_buf(s, s->partial, plan.partial_bytes));
     a.q = const_cast<float *>(d_q) + b0 * (size_t)Hq * D;
     a.cur_k = const_cast<float *>(d_k) + b0 * (size_t)Hkv * D;
     a.cur_v = d_v + b0 * (size_t)Hkv * D;
     a.out = d_out + b0 * (size_t)Hq * D;
-    a.partial = (float *)s->partial.p;
+    a.partial = fixed ? fixed : (float *)s->partial.p;
     a.err = s->d_err;
     a.rope_cos = table ? table->cos : nullptr;
     a.rope_sin = table ? table->sin : nullptr;
@@ -974,17 +1027,78 @@ static int run_generic(spissa_session *s, const float *d_q, const float *d_k, co
   return SPISSA_OK;
 }
 
+// Launch plan of one bf16 prefill call (S > 1 queries over P cached keys):
+// staging geometry, key splits and the head_dim-256 O split, set in `a`
+// (whose P, S, Hq, Hkv, R, causal and window are filled in).
+struct PrefillPlan {
+  int P8 = 0;              // keys below come from the cache's bf16 shadow
+  size_t cap_stage = 0;    // staging rows per KV head (tile-aligned)
+  size_t stage_bytes = 0;  // bf16 K and V^T staging
+  size_t ppart_bytes = 0;  // key-split partials (0: no splits)
+  long tiles = 0;          // most key tiles of one unsplit workgroup
+  size_t workgroups = 0;
+};
+
+static void plan_prefill(PrefillArgs &a, int D, int cus, PrefillPlan *p) {
+  const int P = a.P, S = a.S;
+  // Keys [0, P8) are read from the cache's bf16 shadow, keys [P8, P+S) from
+  // the staging buffer; P8 is tile-aligned so no key tile straddles the two.
+  p->P8 = P & ~(kPrefillTileAlign - 1);
+  p->cap_stage = (((size_t)P + S + kPrefillTileAlign - 1) & ~(size_t)(kPrefillTileAlign - 1)) - p->P8;
+  p->stage_bytes = 2 * (size_t)a.Hkv * p->cap_stage * D * sizeof(bf16);
+  a.P8 = p->P8;
+  a.cap_stage = (long)p->cap_stage;
+  a.splits = 1;
+  a.tps = 0;
+  // Key splits when the unsplit grid cannot fill the GPU (short chunks over
+  // long caches, few heads): enough splits for one round of workgroup slots,
+  // each covering at least four key tiles of its workgroup's range. The
+  // splits cover the widest tile range any workgroup has, so every
+  // workgroup's keys are covered.
+  const long base = prefill_base_workgroups(a, D);
+  const long slots = (long)cus * prefill_wgs_per_cu(D);
+  p->tiles = prefill_max_tile_span(a, D);
+  if (base < slots) {
+    const long want = std::min(std::min((slots + base - 1) / base, p->tiles / 4), (long)D);
+    if (want >= 2) {  // (at most head_dim splits: the measured useful range)
+      a.tps = (int)((p->tiles + want - 1) / want);
+      a.splits = (int)((p->tiles + a.tps - 1) / a.tps);
+      p->ppart_bytes = (size_t)a.splits * S * a.Hq * (D + 2) * sizeof(float);
+    }
+  }
+  // The O split where a workgroup covers at least 32 key tiles (measured:
+  // 10% faster on a 4096-token causal prefill at head_dim 256, 5-9% slower on
+  // windowed and split ranges of 10-19 tiles).
+  a.o_split = D >= 256 && (a.splits > 1 ? a.tps : p->tiles) >= 32;
+  p->workgroups = (size_t)base * a.splits;
+}
+
+static void prefill_args_base(PrefillArgs &a, const spissa_kv_attention_config *c, int P) {
+  memset(&a, 0, sizeof a);
+  a.P = P;
+  a.S = (int)c->query_len;
+  a.Hq = (int)c->num_heads;
+  a.Hkv = (int)c->kv_heads;
+  a.R = a.Hq / a.Hkv;
+  a.causal = c->causal ? 1 : 0;
+  a.window = (int)c->window;
+  a.qk_scale_log2 = (1.0f / sqrtf((float)c->head_dim)) * 1.4426950408889634f;
+}
+
 static int run_prefill(spissa_session *s, const float *d_q, const float *d_k, const float *d_v,
                        spissa_kv_cache *cache, const spissa_kv_attention_config *c, float *d_out) {
   const int D = (int)c->head_dim, Hkv = (int)c->kv_heads;
   const int P = cache ? (int)cache->len : 0;
   const int S = (int)c->query_len;
-  // Keys [0, P8) are read from the cache's bf16 shadow, keys [P8, P+S) from
-  // the staging buffer; P8 is tile-aligned so no key tile straddles the two.
-  const int P8 = P & ~(kPrefillTileAlign - 1);
+  PrefillArgs a;
+  prefill_args_base(a, c, P);
+  PrefillPlan plan;
+  plan_prefill(a, D, s->cus, &plan);
+  const int P8 = plan.P8;
+  const size_t cap_stage = plan.cap_stage;
   if (cache && P8 > 0) ST_TRY(ensure_shadow(cache, s->stream));
-  const size_t cap_stage = (((size_t)P + S + kPrefillTileAlign - 1) & ~(size_t)(kPrefillTileAlign - 1)) - P8;
-  ST_TRY(ensure_buf(s, s->stage, 2 * (size_t)Hkv * cap_stage * D * sizeof(bf16), false));
+  ST_TRY(ensure_buf(s, s->stage, plan.stage_bytes));
+  if (plan.ppart_bytes) ST_TRY(ensure_buf(s, s->ppart, plan.ppart_bytes));
   bf16 *kb_stage = (bf16 *)s->stage.p;
   bf16 *vt_stage = kb_stage + (size_t)Hkv * cap_stage * D;
   const size_t w = (size_t)Hkv * D;
@@ -993,8 +1107,6 @@ static int run_prefill(spissa_session *s, const float *d_q, const float *d_k, co
     HIP_TRY(launch_stage_bf16(s->stream, cache->keys + (size_t)P8 * w, cache->values + (size_t)P8 * w, tail, tail,
                               Hkv, D, kb_stage, vt_stage, 0, cap_stage));
   HIP_TRY(launch_stage_bf16(s->stream, d_k, d_v, S, cap_stage - tail, Hkv, D, kb_stage, vt_stage, tail, cap_stage));
-  PrefillArgs a;
-  memset(&a, 0, sizeof a);
   a.q = d_q;
   a.out = d_out;
   a.kb_cache = cache ? cache->kb : nullptr;
@@ -1002,42 +1114,12 @@ static int run_prefill(spissa_session *s, const float *d_q, const float *d_k, co
   a.kb_stage = kb_stage;
   a.vt_stage = vt_stage;
   a.cap_cache = cache ? (long)cache->shadow_cap : 0;
-  a.cap_stage = (long)cap_stage;
-  a.P = P;
-  a.P8 = P8;
-  a.S = S;
-  a.Hq = (int)c->num_heads;
-  a.Hkv = Hkv;
-  a.R = a.Hq / Hkv;
-  a.causal = c->causal ? 1 : 0;
-  a.window = (int)c->window;
   a.err = s->d_err;
-  a.qk_scale_log2 = (1.0f / sqrtf((float)D)) * 1.4426950408889634f;
-  a.splits = 1;
-  // Key splits when the unsplit grid cannot fill the GPU (short chunks over
-  // long caches, few heads): enough splits for one round of workgroup slots,
-  // each covering at least four key tiles of its workgroup's range.
-  const long base = prefill_base_workgroups(a, D);
-  const long slots = (long)s->cus * prefill_wgs_per_cu(D);
-  const int bn = prefill_tile_keys(D), wgq = prefill_wg_queries(a, D);
-  long keys = (long)P + S;  // widest visible key range of one workgroup
-  if (a.window > 0) keys = std::min(keys, (long)a.window + wgq + bn);
-  const long tiles = (keys + bn - 1) / bn + 1;
-  if (base < slots) {
-    const long want = std::min(std::min((slots + base - 1) / base, tiles / 4), (long)D);
-    if (want >= 2) {  // (at most head_dim splits: the measured useful range)
-      a.tps = (int)((tiles + want - 1) / want);
-      a.splits = (int)((tiles + a.tps - 1) / a.tps);
-      const size_t rows = (size_t)a.splits * S * a.Hq;
-      ST_TRY(ensure_buf(s, s->ppart, rows * (D + 2) * sizeof(float), false));
-      a.part_o = (float *)s->ppart.p;
-      a.part_ml = a.part_o + rows * D;
-    }
+  if (a.splits > 1) {
+    const size_t rows = (size_t)a.splits * S * a.Hq;
+    a.part_o = (float *)s->ppart.p;
+    a.part_ml = a.part_o + rows * D;
   }
-  // The O split where a workgroup covers at least 32 key tiles (measured:
-  // 10% faster on a 4096-token causal prefill at head_dim 256, 5-9% slower on
-  // windowed and split ranges of 10-19 tiles).
-  a.o_split = D >= 256 && (a.splits > 1 ? a.tps : tiles) >= 32;
   HIP_TRY(launch_prefill(s->stream, a, D));
   HIP_TRY(launch_prefill_combine(s->stream, a, D));
   return SPISSA_OK;
@@ -1090,10 +1172,9 @@ extern "C" int spissa_attention_decode_batch_device(spissa_session *s, const flo
   GUARD_END
 }
 
-extern "C" int spissa_decode_step_device(spissa_session *s, const spissa_rope_table *table, const float *d_q,
-                                         const float *d_k, const float *d_v, spissa_kv_cache *const *caches,
-                                         size_t batch, const spissa_kv_attention_config *cfg, float *d_out) {
-  GUARD_BEGIN
+// Every check of a fused decode step, before anything runs.
+static int validate_decode_step(spissa_session *s, const spissa_rope_table *table, spissa_kv_cache *const *caches,
+                                size_t batch, const spissa_kv_attention_config *cfg) {
   if (!s || !cfg || !caches) return set_err(SPISSA_ERR_ARGUMENT, "null argument");
   if (cfg->query_len != 1) return set_err(SPISSA_ERR_SHAPE, "a decode step needs query_len == 1, got %zu", cfg->query_len);
   for (size_t b = 0; b < batch; ++b) {
@@ -1106,6 +1187,12 @@ extern "C" int spissa_decode_step_device(spissa_session *s, const spissa_rope_ta
     if (!decode_cache_fits(caches[b]))
       return set_err(SPISSA_ERR_SHAPE, "cache %zu exceeds the fused decode step's 4 GiB per-buffer limit", b);
   }
+  // Each sequence appends one row at its own length: a cache listed twice
+  // would have both tokens written to the same row.
+  std::vector<const spissa_kv_cache *> seen(caches, caches + batch);
+  std::sort(seen.begin(), seen.end());
+  if (std::adjacent_find(seen.begin(), seen.end()) != seen.end())
+    return set_err(SPISSA_ERR_ARGUMENT, "a cache appears more than once in one decode step");
   const int D = (int)cfg->head_dim;
   if (!decode_supported(D, (int)(cfg->num_heads / cfg->kv_heads)))
     return set_err(SPISSA_ERR_SHAPE, "the fused decode step supports head_dim 64, 128 and 256, got %d", D);
@@ -1117,10 +1204,73 @@ extern "C" int spissa_decode_step_device(spissa_session *s, const spissa_rope_ta
         return set_err(SPISSA_ERR_SHAPE, "position %zu exceeds the rope table (%zu positions)", caches[b]->len,
                        table->max_positions);
   }
+  return SPISSA_OK;
+}
+
+extern "C" int spissa_decode_step_device(spissa_session *s, const spissa_rope_table *table, const float *d_q,
+                                         const float *d_k, const float *d_v, spissa_kv_cache *const *caches,
+                                         size_t batch, const spissa_kv_attention_config *cfg, float *d_out) {
+  GUARD_BEGIN
+  ST_TRY(validate_decode_step(s, table, caches, batch, cfg));
   if (batch == 0) return SPISSA_OK;
   HIP_TRY(hipSetDevice(s->device));
   ST_TRY(run_decode(s, d_q, d_k, d_v, caches, batch, cfg, d_out, table, true));
   for (size_t b = 0; b < batch; ++b) caches[b]->len += 1;
+  return SPISSA_OK;
+  GUARD_END
+}
+
+extern "C" int spissa_plan_attention(const spissa_kv_attention_config *cfg, const size_t *past_lens, size_t batch,
+                                     int compute_units, int prefill_precision, spissa_attention_plan *out) {
+  GUARD_BEGIN
+  if (!cfg || !past_lens || !out) return set_err(SPISSA_ERR_ARGUMENT, "null argument");
+  if (batch == 0) return set_err(SPISSA_ERR_ARGUMENT, "a plan needs at least one sequence");
+  if (batch > 1 && cfg->query_len != 1)
+    return set_err(SPISSA_ERR_SHAPE, "several sequences need query_len == 1, got %zu", cfg->query_len);
+  ST_TRY(validate_attention(0, 0, 0, nullptr, cfg, false));
+  for (size_t b = 0; b < batch; ++b)
+    if (past_lens[b] > (size_t)INT32_MAX / 2 - cfg->query_len)
+      return set_err(SPISSA_ERR_SHAPE, "attention sizes exceed the device kernels' limits");
+  memset(out, 0, sizeof *out);
+  const int D = (int)cfg->head_dim, Hq = (int)cfg->num_heads, Hkv = (int)cfg->kv_heads;
+  const int cus = compute_units > 0 ? compute_units : 256;
+  if (cfg->query_len == 1 && decode_supported(D, Hq / Hkv)) {
+    out->path = SPISSA_KERNEL_DECODE;
+    for (size_t b0 = 0; b0 < batch; b0 += kMaxDecodeBatch) {
+      const int B = (int)std::min<size_t>(kMaxDecodeBatch, batch - b0);
+      int past[kMaxDecodeBatch];
+      for (int b = 0; b < B; ++b) past[b] = (int)past_lens[b0 + b];
+      DecodePlan p;
+      plan_decode(D, Hq, Hkv, cfg->window, past, B, 0, &p);
+      if (b0 == 0) {
+        out->heads_per_block = p.RB;
+        out->head_blocks = p.HB;
+        out->keys_per_split = p.kps;
+        out->splits = p.max_splits;
+        out->workgroups = p.workgroups;
+      }
+      out->partial_bytes = std::max(out->partial_bytes, p.partial_bytes);
+    }
+    return SPISSA_OK;
+  }
+  if (cfg->query_len > 1 && prefill_precision == SPISSA_PREFILL_BF16 && prefill_supported(D)) {
+    out->path = SPISSA_KERNEL_PREFILL_BF16;
+    PrefillArgs a;
+    prefill_args_base(a, cfg, (int)past_lens[0]);
+    PrefillPlan p;
+    plan_prefill(a, D, cus, &p);
+    out->splits = a.splits;
+    out->tiles_per_split = a.tps;
+    out->tile_keys = prefill_tile_keys(D);
+    out->workgroup_queries = prefill_wg_queries(a, D);
+    out->o_split = a.o_split;
+    out->max_tiles = p.tiles;
+    out->workgroups = p.workgroups;
+    out->partial_bytes = p.ppart_bytes;
+    out->stage_bytes = p.stage_bytes;
+    return SPISSA_OK;
+  }
+  out->path = SPISSA_KERNEL_GENERIC;
   return SPISSA_OK;
   GUARD_END
 }
@@ -1337,7 +1487,7 @@ static int argmax_launch(spissa_session *s, const float *d_x, size_t n, int64_t 
   // ops.rs:326-332: no exclusion, an out-of-range one, or a single logit is
   // plain sample_argmax
   const int excl = (excluded < 0 || (uint64_t)excluded >= n || n <= 1) ? -1 : (int)excluded;
-  ST_TRY(ensure_buf(s, s->amax, kArgmaxMaxParts * sizeof(ArgmaxPart), false));
+  ST_TRY(ensure_buf(s, s->amax, kArgmaxMaxParts * sizeof(ArgmaxPart)));
   HIP_TRY(hipSetDevice(s->device));
   HIP_TRY(launch_argmax(s->stream, d_x, (int)n, excl, (ArgmaxPart *)s->amax.p, d_token));
   return SPISSA_OK;
@@ -1470,7 +1620,7 @@ extern "C" int spissa_attention_sublayer_device(spissa_session *s, const spissa_
                            L->d_post_norm ? S * H : 0};
   size_t total = 0;
   for (size_t n : sizes) total += (n + 63) & ~(size_t)63;
-  ST_TRY(ensure_buf(s, s->sub, std::max<size_t>(total, 64) * sizeof(float), false));
+  ST_TRY(ensure_buf(s, s->sub, std::max<size_t>(total, 64) * sizeof(float)));
   float *r[6];
   {
     float *p = (float *)s->sub.p;

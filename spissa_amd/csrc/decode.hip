@@ -28,6 +28,7 @@
 //
 // Errors. A zero or non-finite softmax denominator (rotary.rs:560-564) sets a
 // device error bit instead of aborting.
+#include <algorithm>
 #include <cstdlib>
 
 #include "internal.hpp"
@@ -481,7 +482,7 @@ hipError_t launch_d(hipStream_t st, const DecodeArgs &a, int RB) {
 
 bool decode_supported(int D, int R) { return (D == 64 || D == 128 || D == 256) && R >= 1; }
 
-int decode_keys_per_split(int D, int RB, long total_rows, int max_keys) {
+int decode_keys_per_split(int D, int RB, long total_rows, int max_keys, int split_cap) {
   const int chunk = 4 * (64 / (D / 8)) * rows_per_group(RB);  // keys of one workgroup iteration
   // about 1024 workgroups over the launch (grids of exactly 3 or 4 per CU
   // measured no faster)
@@ -489,8 +490,13 @@ int decode_keys_per_split(int D, int RB, long total_rows, int max_keys) {
   const long per = (total_rows + target - 1) / target;
   long kps = ((per + chunk - 1) / chunk) * chunk;
   if (kps < chunk) kps = chunk;
-  // Bound the partials the combine kernel reads per output.
-  while ((max_keys + kps - 1) / kps > kMaxDecodeSplits) kps += chunk;
+  // Bound the partials the combine kernel reads per output (and the caller's
+  // partial buffer).
+  const long cap = std::max(1, std::min(split_cap, kMaxDecodeSplits));
+  if ((max_keys + kps - 1) / kps > cap) {
+    const long need = (max_keys + cap - 1) / cap;
+    kps = ((need + chunk - 1) / chunk) * chunk;
+  }
   return (int)kps;
 }
 

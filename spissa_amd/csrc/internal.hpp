@@ -116,6 +116,8 @@ int prefill_tile_keys(int D);
 int prefill_wg_queries(const PrefillArgs &a, int D);
 // Workgroups one (unsplit) prefill launch would have.
 long prefill_base_workgroups(const PrefillArgs &a, int D);
+// Most key tiles one (unsplit) prefill workgroup visits.
+long prefill_max_tile_span(const PrefillArgs &a, int D);
 
 struct GenericArgs {
   const float *q;  // [S, Hq, D]
@@ -180,8 +182,10 @@ constexpr int kArgmaxMaxParts = 1024;  // partials one launch writes at most
 hipError_t launch_argmax(hipStream_t st, const float *x, int n, int excl, ArgmaxPart *parts, int *token);
 
 // Keys per split of a decode launch: total_rows = key rows summed over all
-// (sequence, KV head, head block) triples; max_keys = longest visible range.
-int decode_keys_per_split(int D, int RB, long total_rows, int max_keys);
+// (sequence, KV head, head block) triples; max_keys = longest visible range;
+// the longest range gets at most split_cap splits (and never more than
+// kMaxDecodeSplits).
+int decode_keys_per_split(int D, int RB, long total_rows, int max_keys, int split_cap);
 bool decode_supported(int D, int R);
 bool prefill_supported(int D);
 

@@ -55,6 +55,7 @@
 // This file is compiled with MFMA results in VGPRs (-amdgpu-mfma-vgpr-form):
 // the score accumulators feed VALU code directly instead of round-tripping
 // through AGPRs.
+#include <algorithm>
 #include <type_traits>
 
 #include "internal.hpp"
@@ -645,6 +646,26 @@ long prefill_base_workgroups(const PrefillArgs &a, int D) {
   const int wgq = prefill_wg_queries(a, D);
   const int rb = 128 / wgq;
   return (long)((a.S + wgq - 1) / wgq) * a.Hkv * (a.R / rb);
+}
+
+// The largest t_end - t_begin of prefill_kernel over its query blocks, with
+// the kernel's own range arithmetic: causal blocks end at their last query,
+// non-causal ones at the last key; a window starts each block at its first
+// query's window.
+long prefill_max_tile_span(const PrefillArgs &a, int D) {
+  const long wgq = prefill_wg_queries(a, D), bn = prefill_tile_keys(D);
+  const long key_total = (long)a.P + a.S;
+  const long nq = (a.S + wgq - 1) / wgq;
+  long span = 0;
+  for (long qt = 0; qt < nq; ++qt) {
+    const long p0 = qt * wgq;
+    long key_end = key_total;
+    if (a.causal) key_end = std::min(key_total, (long)a.P + std::min((long)a.S, p0 + wgq));
+    long key_begin = 0;
+    if (a.window > 0) key_begin = std::max(0L, (long)a.P + p0 - a.window + 1);
+    span = std::max(span, (key_end + bn - 1) / bn - key_begin / bn);
+  }
+  return span;
 }
 
 // Merges key splits: per (query row, head), M = max m_j, then

@@ -41,6 +41,20 @@ def _dev_i32(t, name: str) -> int:
     return t.data_ptr()
 
 
+def plan_attention(config: KvAttentionConfig, past_lens: Sequence[int], compute_units: int = 256,
+                   precision: int = _ffi.PREFILL_BF16) -> dict:
+    """The launch geometry spissa_plan_attention reports for one attention call
+    (no device needed): kernel path, decode head blocks and key splits, prefill
+    tiles and key splits, grid and workspace bytes."""
+    lib = _ffi.load()
+    past = (_ffi.c_size * max(1, len(past_lens)))(*past_lens)
+    cfg = config._c()
+    plan = _ffi.AttentionPlanC()
+    check(lib.spissa_plan_attention(C.byref(cfg), past, len(past_lens), compute_units, precision,
+                                    C.byref(plan)))
+    return {name: getattr(plan, name) for name, _ in _ffi.AttentionPlanC._fields_}
+
+
 class RopeTable:
     """A resident cos/sin table (spissa_rope_table_new)."""
 

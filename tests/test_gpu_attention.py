@@ -326,3 +326,71 @@ def test_fused_decode_batch_after_prefill_keeps_shadow_consistent(gpu):
     q, k, v, _, _ = layer_inputs(25, 0, 9, 0, Hq, Hkv, D)
     got = gpu.scaled_dot_product_attention_with_cache(q, k, v, caches[0], gpu.KvAttentionConfig(9, Hq, Hkv, D, True))
     assert rel_err(got, o.sdpa_with_cache(q, k, v, refs[0], 9, Hq, Hkv, D)) <= BF16_TOL
+
+
+@pytest.mark.parametrize("S,P,Hq,Hkv,D,W", [(256, 4100, 32, 8, 64, 512), (128, 3000, 16, 4, 128, 1024)])
+def test_prefill_windowed_non_causal_with_key_splits(gpu, S, P, Hq, Hkv, D, W):
+    """A windowed non-causal chunk over a long cache takes key splits, and a
+    block's range then runs from its first query's window to the last key:
+    every split range must be covered (the oracle applies the same window)."""
+    print(f"[case] prefill non-causal window S={S} P={P} Hq={Hq} Hkv={Hkv} D={D} W={W}", flush=True)
+    got, ref, _, _ = run_both(gpu, 26, S, S, P, Hq, Hkv, D, W, causal=False)
+    assert rel_err(got, ref) <= BF16_TOL
+
+
+def test_decode_step_rejects_a_cache_listed_twice(gpu):
+    import torch
+
+    from spissa_amd.device import Session
+
+    Hq, Hkv, D = 8, 2, 64
+    s = Session(0)
+    c0, c1 = s.kv_cache(Hkv, D, 8), s.kv_cache(Hkv, D, 8)
+    q = torch.zeros(3, Hq, D, device="cuda")
+    k = torch.zeros(3, Hkv, D, device="cuda")
+    out = torch.empty_like(q)
+    with pytest.raises(gpu.ArgumentError):
+        s.decode_step(None, q, k, k.clone(), [c0, c1, c0], gpu.KvAttentionConfig(1, Hq, Hkv, D, True), out)
+    assert c0.len() == 0 and c1.len() == 0  # nothing appended
+    s.decode_step(None, q[:2], k[:2], k[:2].clone(), [c0, c1], gpu.KvAttentionConfig(1, Hq, Hkv, D, True), out[:2])
+    s.sync()
+    assert c0.len() == 1 and c1.len() == 1
+
+
+def test_workspace_growth_under_graph_capture_is_a_clear_error(gpu):
+    """A call whose workspace would grow while its stream is captured returns
+    ERR_ARGUMENT with a message instead of a device error; the same call
+    after an uncaptured warm-up captures and replays."""
+    import torch
+
+    from spissa_amd.device import Session
+
+    S, Hq, Hkv, D = 64, 8, 2, 128
+    st = torch.cuda.Stream()
+    s = Session(0, stream=st)
+    q = torch.randn(S, Hq, D, device="cuda")
+    k = torch.randn(S, Hkv, D, device="cuda")
+    v = torch.randn(S, Hkv, D, device="cuda")
+    out = torch.empty_like(q)
+    cfg = gpu.KvAttentionConfig(S, Hq, Hkv, D, True)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    raised = None
+    with torch.cuda.graph(g, stream=st):
+        try:
+            s.attention(q, k, v, None, cfg, out)
+        except gpu.ArgumentError as e:
+            raised = str(e)
+    assert raised is not None and "captured" in raised, raised
+    s.attention(q, k, v, None, cfg, out)  # warm-up: the workspace grows here
+    s.sync()
+    want = out.clone()
+    out.zero_()
+    g2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g2, stream=st):
+        s.attention(q, k, v, None, cfg, out)
+    for _ in range(3):
+        out.zero_()
+        g2.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want)

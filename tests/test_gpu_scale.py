@@ -1,10 +1,11 @@
 """GPU parity at the BASELINE configurations' full sizes.
 
-The oracle is single-threaded C; at full size it is run only where it
+The oracle is C, one call per thread; at full size it is run only where it
 finishes in seconds:
-  * a prefill's first and last query rows, as chunked calls: a call with the
-    earlier rows in the cache computes those rows exactly as the one-shot call
-    does (same keys, same loop order, rotary.rs:335-415);
+  * blocks of a prefill's query rows spread evenly over the prompt (the first,
+    the last and eight between), as chunked calls: a call with the earlier
+    rows in the cache computes those rows exactly as the one-shot call does
+    (same keys, same loop order, rotary.rs:335-415);
   * single-token decode (tens of milliseconds per call);
   * cache contents, which are bitwise.
 Size-independent properties cover the rest: the bf16-MFMA prefill against the
@@ -47,6 +48,29 @@ def oracle_rows(q, k, v, S, Hq, Hkv, D, lo, hi, window=0, past_k=None, past_v=No
                              hi - lo, Hq, Hkv, D, True, window)
 
 
+def spaced_blocks(S, rows, count=10):
+    """`count` blocks of `rows` query rows spread evenly over [0, S), both ends included."""
+    return [(lo, lo + rows) for lo in sorted({(i * (S - rows)) // (count - 1) for i in range(count)})]
+
+
+def oracle_blocks(q, k, v, Hq, Hkv, D, blocks, window=0, past_k=None, past_v=None, threads=16):
+    """Oracle output rows [lo, hi) of a causal call for every block, each as a
+    chunked call (the rows before lo in the cache), run on `threads` threads."""
+    P = 0 if past_k is None else past_k.size // (Hkv * D)
+    w, wq = Hkv * D, Hq * D
+    units = []
+    for lo, hi in blocks:
+        cache = o.KvCache(Hkv, D, P + hi)
+        if P:
+            cache.append(past_k, past_v, P)
+        if lo:
+            cache.append(k[:lo * w].copy(), v[:lo * w].copy(), lo)
+        units.append((q[lo * wq:hi * wq].copy(), k[lo * w:hi * w].copy(), v[lo * w:hi * w].copy(), cache))
+    rows = blocks[0][1] - blocks[0][0]
+    assert all(hi - lo == rows for lo, hi in blocks)
+    return o.sdpa_many(units, (rows, Hq, Hkv, D, 1, window), threads)
+
+
 def device_attention(s, q, k, v, cache, S, Hq, Hkv, D, window=0, precision=None):
     torch = _torch()
     from spissa_amd.rotary import KvAttentionConfig
@@ -79,8 +103,11 @@ def test_full_prefill_rows_and_f32_cross_check(gpu, name, S, Hq, Hkv, D, window)
     assert np.all(np.isfinite(got))
     assert rel_err(got, f32) <= BF16_TOL, "bf16 prefill vs the device f32 path, all rows"
     wq = Hq * D
-    for lo, hi in ((0, 48), (S - 48, S)):
-        ref = oracle_rows(q, k, v, S, Hq, Hkv, D, lo, hi, window)
+    # ten 32-row query blocks spread over the prompt (first, last and eight
+    # between, at offsets that are not tile-aligned), each against the oracle
+    blocks = spaced_blocks(S, 32)
+    refs = oracle_blocks(q, k, v, Hq, Hkv, D, blocks, window)
+    for (lo, hi), ref in zip(blocks, refs):
         assert rel_err(_rows(got, S, wq, lo, hi), ref) <= BF16_TOL, (lo, hi)
         assert rel_err(_rows(f32, S, wq, lo, hi), ref) <= DECODE_TOL, ("f32 path", lo, hi)
 
@@ -176,21 +203,23 @@ def test_cfg2_prefill_2048_then_128_decode_steps(gpu):
 
 def test_cfg5_chunk_128_on_16384_then_decode(gpu):
     """Gemma-3-4B resident cache: 16384 cached tokens, a 128-token chunk (global
-    and local W1024 layers), then decode steps appending to the same cache."""
+    and local W1024 layers), then all 256 decode steps of the workload
+    appending to the same cache, with the cache bytes checked bitwise."""
     torch = _torch()
     from spissa_amd.device import Session
     from spissa_amd.rotary import KvAttentionConfig
 
-    print("[case] cfg5 chunk 128 on 16384 + decode", flush=True)
-    Hq, Hkv, D, P, S, steps = 8, 4, 256, 16384, 128, 16
+    print("[case] cfg5 chunk 128 on 16384 + 256 decode steps", flush=True)
+    Hq, Hkv, D, P, S, steps = 8, 4, 256, 16384, 128, 256
     s = Session(0)
     for window in (0, 1024):
         q, k, v, pk, pv = layer_inputs(34, window, S, P, Hq, Hkv, D)
         cache = s.kv_cache(Hkv, D, P + S + steps)
         cache.append(pk, pv, P)
         got = device_attention(s, q, k, v, cache, S, Hq, Hkv, D, window)
-        for lo, hi in ((0, 16), (S - 16, S)):
-            ref = oracle_rows(q, k, v, S, Hq, Hkv, D, lo, hi, window, past_k=pk, past_v=pv)
+        blocks = spaced_blocks(S, 16, count=8)
+        refs = oracle_blocks(q, k, v, Hq, Hkv, D, blocks, window, past_k=pk, past_v=pv)
+        for (lo, hi), ref in zip(blocks, refs):
             assert rel_err(_rows(got, S, Hq * D, lo, hi), ref) <= BF16_TOL, (window, lo, hi)
         cache.append(k, v, S)
         ref_cache = o.KvCache(Hkv, D, P + S + steps)
@@ -235,3 +264,53 @@ def test_cache_over_4GiB_per_buffer_uses_generic_decode(gpu):
                       torch.empty_like(d1[0]))
     assert cache.len() == P
     del cache
+
+
+@pytest.mark.parametrize("name,base,divisor,window", [
+    ("global theta 1e6 divisor 8", 1000000.0, 8.0, 0),
+    ("local theta 1e4 W512", 10000.0, 1.0, 512),
+])
+def test_cfg4_gemma_qk_norm_rope_decode_at_32768(gpu, name, base, divisor, window):
+    """Gemma-3-1B decode at 32768 cached tokens with the whole layer prologue
+    (models/gemma/generate.rs:232-295): QK-norm of the new q and k rows
+    (ops.rs:159-179), Gemma RoPE at position 32768 (rotary.rs:137-186), the
+    x1.0 prescale, attention over the cache (global, or the W512 window), then
+    the append. The cached keys went through the same prologue at their own
+    positions. Prologue bitwise, output <= 1e-4 against the oracle."""
+    torch = _torch()
+    from spissa_amd import _ffi
+    from spissa_amd.device import Session
+    from spissa_amd.rotary import KvAttentionConfig
+    from spissa_amd.synth import normal_f32, seed_for
+
+    print(f"[case] cfg4 gemma-1B QK-norm + RoPE + decode @32768 {name}", flush=True)
+    Hq, Hkv, D, P, eps = 4, 1, 256, 32768, 1e-6
+    q, k, v, pk, pv = layer_inputs(37, window, 1, P, Hq, Hkv, D)
+    qn = normal_f32(seed_for(37, window, 0, "qnorm"), D, 1.0, 0.1)
+    kn = normal_f32(seed_for(37, window, 0, "knorm"), D, 1.0, 0.1)
+    # cached keys: normed and rotated at positions 0..P-1 (the past prologues)
+    dummy = np.zeros(P * D, dtype=np.float32)
+    o.gemma_qk_prologue(dummy, pk, P, 1, Hkv, D, qn, kn, eps, base, divisor, 0, float(D))
+    ref_cache = o.KvCache(Hkv, D, P + 1)
+    ref_cache.append(pk, pv, P)
+    rq, rk = q.copy(), k.copy()
+    o.gemma_qk_prologue(rq, rk, 1, Hq, Hkv, D, qn, kn, eps, base, divisor, P, float(D))
+    want = o.sdpa_with_cache(rq, rk, v, ref_cache, 1, Hq, Hkv, D, True, window)
+    ref_cache.append(rk, v, 1)
+
+    s = Session(0)
+    table = s.rope_table(_ffi.ROPE_GEMMA, D, base, position_divisor=divisor, max_positions=P + 8)
+    cache = s.kv_cache(Hkv, D, P + 1)
+    cache.append(pk, pv, P)
+    dq, dk, dv, dqn, dkn = (torch.from_numpy(x).cuda() for x in (q, k, v, qn, kn))
+    s.gemma_qk_prologue(table, dq, dk, 1, Hq, Hkv, D, dqn, dkn, eps, P, 1.0)
+    out = torch.empty_like(dq)
+    s.attention(dq, dk, dv, cache, KvAttentionConfig(1, Hq, Hkv, D, True, window), out)
+    s.append(cache, dk, dv, 1)
+    s.sync()
+    assert_bitwise(dq.cpu().numpy(), rq, "prologue q")
+    assert_bitwise(dk.cpu().numpy(), rk, "prologue k")
+    err = rel_err(out.cpu().numpy(), want)
+    print(f"[gemma] decode @32768 {name}: rel err {err:.2e}", flush=True)
+    assert err <= DECODE_TOL
+    assert_bitwise(cache.keys()[P * D:], ref_cache.keys()[P * D:], "appended key")

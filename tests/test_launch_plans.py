@@ -1,0 +1,192 @@
+"""CPU checks of the host launch arithmetic (spissa_plan_attention) against the
+kernels' own index ranges, with no GPU.
+
+For every plan the library reports, this replays what each workgroup of the
+kernel would read and write, using the range formulas of decode_split_kernel
+and decode_combine_kernel (decode.hip) and prefill_kernel (prefill.hip), and
+checks that
+  - the splits of every (sequence, head) cover exactly the keys its queries
+    may see (rotary.rs:355,362-365 causal mask, plus the window), once each;
+  - every partial a split writes, and every staged row the prefill reads, lies
+    inside the workspace the plan sizes.
+Shapes: every BASELINE config, the windowed non-causal chunks that once
+dropped key tiles, and a seeded sweep.
+"""
+import random
+
+import pytest
+
+from spissa_amd import _ffi
+from spissa_amd.device import plan_attention
+from spissa_amd.rotary import KvAttentionConfig
+
+MAX_DECODE_BATCH = 16
+MAX_DECODE_SPLITS = 512
+TILE_ALIGN = 64
+
+
+def check_decode(cfg, past, plan):
+    """decode_split_kernel: grid (Hkv*HB, max_splits, B); split s of sequence b
+    covers cached keys [kstart + s*kps, min(P, kstart + (s+1)*kps)) where
+    kstart = max(0, P + 1 - W) with a window; the new token is the combine's."""
+    D, Hq, Hkv, W = cfg.head_dim, cfg.num_heads, cfg.kv_heads, cfg.window
+    assert plan["path"] == _ffi.KERNEL_DECODE
+    RB, HB, kps = plan["heads_per_block"], plan["head_blocks"], plan["keys_per_split"]
+    assert RB * HB == Hq // Hkv and kps > 0
+    entry = RB * (D + 2)
+    B = min(len(past), MAX_DECODE_BATCH)  # the plan describes the first launch
+    max_splits = plan["splits"]
+    assert max_splits <= MAX_DECODE_SPLITS
+    assert plan["workgroups"] == B * Hkv * HB * max_splits
+    groups = B * Hkv * HB
+    assert plan["partial_bytes"] >= groups * max(1, max_splits) * entry * 4
+    for b in range(B):
+        P = past[b]
+        kstart = max(0, P + 1 - W) if W > 0 else 0
+        nsplit = -(-(P - kstart) // kps)
+        assert nsplit <= max_splits
+        covered = []
+        for s in range(nsplit):
+            k0 = kstart + s * kps
+            k1 = min(P, k0 + kps)
+            assert k0 < k1
+            covered.append((k0, k1))
+            for h in range(Hkv):
+                for hb in range(HB):
+                    bhh = (b * Hkv + h) * HB + hb
+                    end = ((bhh * max_splits + s) + 1) * entry  # floats written by this split
+                    assert end * 4 <= plan["partial_bytes"]
+        # contiguous, disjoint, exactly [kstart, P)
+        pos = kstart
+        for k0, k1 in covered:
+            assert k0 == pos
+            pos = k1
+        assert pos == P
+
+
+def check_prefill(cfg, P, plan):
+    """prefill_kernel: workgroup (qt, split) of a head block covers key tiles
+    [t_begin + split*tps, min(t_end, t_begin + (split+1)*tps)) of its query
+    block's range [t_begin, t_end)."""
+    D, S, Hq, Hkv, W, causal = (cfg.head_dim, cfg.query_len, cfg.num_heads, cfg.kv_heads, cfg.window,
+                                cfg.causal)
+    assert plan["path"] == _ffi.KERNEL_PREFILL_BF16
+    BN, WGQ = plan["tile_keys"], plan["workgroup_queries"]
+    splits, tps = plan["splits"], plan["tiles_per_split"]
+    assert TILE_ALIGN % BN == 0
+    key_total = P + S
+    n_qblocks = -(-S // WGQ)
+    rb = 128 // WGQ
+    assert plan["workgroups"] == n_qblocks * Hkv * (Hq // Hkv // rb) * splits
+    P8 = P & ~(TILE_ALIGN - 1)
+    cap_stage = ((P + S + TILE_ALIGN - 1) & ~(TILE_ALIGN - 1)) - P8
+    assert plan["stage_bytes"] == 2 * Hkv * cap_stage * D * 2
+    if splits > 1:
+        assert plan["partial_bytes"] == splits * S * Hq * (D + 2) * 4
+    else:
+        assert plan["partial_bytes"] == 0
+    widest = 0
+    for qt in range(n_qblocks):
+        p0 = qt * WGQ
+        key_end = min(key_total, P + min(S, p0 + WGQ)) if causal else key_total
+        key_begin = max(0, P + p0 - W + 1) if W > 0 else 0
+        t_begin, t_end = key_begin // BN, -(-key_end // BN)
+        widest = max(widest, t_end - t_begin)
+        # the keys any query of the block may see lie inside [t_begin, t_end) tiles
+        for i in (p0, min(S, p0 + WGQ) - 1):
+            lo = max(0, P + i - W + 1) if W > 0 else 0
+            hi = P + i if causal else key_total - 1
+            if lo <= hi:
+                assert t_begin * BN <= lo and hi < t_end * BN
+        # the splits cover every tile of the block's range, once
+        seen = []
+        for split in range(splits):
+            tb = t_begin + (split * tps if splits > 1 else 0)
+            te = min(t_end, tb + tps) if splits > 1 else t_end
+            seen.extend(range(tb, te))
+        assert seen == list(range(t_begin, t_end)), (qt, t_begin, t_end, splits, tps)
+        # staged rows the block reads stay inside the staging buffer
+        if t_end * BN > P8:
+            assert t_end * BN - P8 <= cap_stage
+    assert widest == plan["max_tiles"]
+
+
+BASELINE_DECODE = [  # (name, Hq, Hkv, D, past lens, window)
+    ("cfg0 llama-1B @512", 32, 8, 64, [512], 0),
+    ("cfg1 llama-1B @2048..2175", 32, 8, 64, [2175], 0),
+    ("cfg2b llama-3B @8192 b1", 24, 8, 128, [8192], 0),
+    ("cfg2b llama-3B @8192 b16", 24, 8, 128, [8192] * 16, 0),
+    ("cfg3 gemma-1B global @32768", 4, 1, 256, [32768], 0),
+    ("cfg3 gemma-1B local W512", 4, 1, 256, [32768], 512),
+    ("cfg4 gemma-4B global @16640", 8, 4, 256, [16640], 0),
+    ("cfg4 gemma-4B local W1024", 8, 4, 256, [16640], 1024),
+    ("ragged batch of 40", 24, 8, 128, [random.Random(3).randrange(0, 9000) for _ in range(40)], 0),
+    ("one long, fifteen short", 32, 8, 256, [16384] + [64] * 15, 0),
+    ("first token", 24, 8, 128, [0, 0, 0], 0),
+]
+
+BASELINE_PREFILL = [  # (name, S, P, Hq, Hkv, D, window, causal)
+    ("cfg1 llama-1B prefill 2048", 2048, 0, 32, 8, 64, 0, True),
+    ("cfg2a llama-3B prefill 4096", 4096, 0, 24, 8, 128, 0, True),
+    ("cfg3 gemma-1B prefill global", 4096, 0, 4, 1, 256, 0, True),
+    ("cfg3 gemma-1B prefill local W512", 4096, 0, 4, 1, 256, 512, True),
+    ("cfg4 gemma-4B chunk global", 128, 16384, 8, 4, 256, 0, True),
+    ("cfg4 gemma-4B chunk local W1024", 128, 16384, 8, 4, 256, 1024, True),
+    # windowed non-causal chunks whose split plan once covered too few tiles
+    ("non-causal W512 over 4100", 256, 4100, 32, 8, 64, 512, False),
+    ("non-causal W1024 over 8000", 512, 8000, 32, 8, 128, 1024, False),
+    ("non-causal W256 d256", 200, 3000, 8, 4, 256, 256, False),
+]
+
+
+@pytest.mark.parametrize("name,Hq,Hkv,D,past,W", BASELINE_DECODE, ids=[c[0] for c in BASELINE_DECODE])
+def test_decode_plan_covers_every_key(name, Hq, Hkv, D, past, W):
+    cfg = KvAttentionConfig(1, Hq, Hkv, D, True, W)
+    plan = plan_attention(cfg, past)
+    for b0 in range(0, len(past), MAX_DECODE_BATCH):  # each launch of <= 16 sequences
+        chunk = past[b0:b0 + MAX_DECODE_BATCH]
+        check_decode(cfg, chunk, plan_attention(cfg, chunk))
+    assert plan["partial_bytes"] >= max(
+        plan_attention(cfg, past[b0:b0 + MAX_DECODE_BATCH])["partial_bytes"]
+        for b0 in range(0, len(past), MAX_DECODE_BATCH))
+
+
+@pytest.mark.parametrize("name,S,P,Hq,Hkv,D,W,causal", BASELINE_PREFILL, ids=[c[0] for c in BASELINE_PREFILL])
+def test_prefill_plan_covers_every_key(name, S, P, Hq, Hkv, D, W, causal):
+    cfg = KvAttentionConfig(S, Hq, Hkv, D, causal, W)
+    check_prefill(cfg, P, plan_attention(cfg, [P]))
+
+
+def test_prefill_plan_sweep():
+    rng = random.Random(20261202)
+    for _ in range(300):
+        D = rng.choice([64, 128, 256])
+        Hkv = rng.choice([1, 2, 4, 8])
+        Hq = Hkv * rng.choice([1, 2, 3, 4, 8])
+        S = rng.choice([2, 33, 64, 128, 257, 1000, 4096])
+        P = rng.choice([0, 5, 64, 100, 2048, 4100, 16384])
+        W = rng.choice([0, 0, 1, 17, 64, 512, 1024, 5000])
+        causal = rng.random() < 0.7
+        cus = rng.choice([256, 80, 304])
+        cfg = KvAttentionConfig(S, Hq, Hkv, D, causal, W)
+        check_prefill(cfg, P, plan_attention(cfg, [P], compute_units=cus))
+
+
+def test_decode_plan_sweep():
+    rng = random.Random(7)
+    for _ in range(200):
+        D = rng.choice([64, 128, 256])
+        Hkv = rng.choice([1, 2, 4, 8])
+        Hq = Hkv * rng.choice([1, 2, 3, 4, 5, 8])
+        B = rng.choice([1, 2, 7, 16])
+        past = [rng.choice([0, 1, 47, 512, 8191, 32768]) for _ in range(B)]
+        W = rng.choice([0, 0, 1, 100, 1024])
+        cfg = KvAttentionConfig(1, Hq, Hkv, D, True, W)
+        check_decode(cfg, past, plan_attention(cfg, past))
+
+
+def test_plan_paths():
+    assert plan_attention(KvAttentionConfig(1, 6, 3, 48, True), [10])["path"] == _ffi.KERNEL_GENERIC
+    assert plan_attention(KvAttentionConfig(8, 6, 3, 128, True), [10],
+                          precision=_ffi.PREFILL_F32)["path"] == _ffi.KERNEL_GENERIC
+    assert plan_attention(KvAttentionConfig(8, 6, 3, 128, True), [10])["path"] == _ffi.KERNEL_PREFILL_BF16
