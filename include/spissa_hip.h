@@ -221,6 +221,21 @@ int spissa_decode_step_device(spissa_session *s, const spissa_rope_table *table,
                               const float *d_q, const float *d_k, const float *d_v,
                               spissa_kv_cache *const *caches, size_t batch,
                               const spissa_kv_attention_config *cfg, float *d_out);
+/* spissa_decode_step_device without any allocation. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops). The split partials live in a
+ * static 8 MiB device array, one copy per GPU (looked up when a session is
+ * created), shared by every call of this function on that GPU: calls that
+ * overlap on one GPU (on different streams) race. Splits are coarsened to
+ * fit; a launch whose one-split-per-head partials (up to 16 sequences x
+ * num_heads x (head_dim + 2) floats) exceed the array is rejected with
+ * SPISSA_ERR_SHAPE before anything runs. Same arguments, checks and results as
+ * spissa_decode_step_device. */
+int spissa_decode_step_device_noalloc(spissa_session *s, const spissa_rope_table *table,
+                                      const float *d_q, const float *d_k, const float *d_v,
+                                      spissa_kv_cache *const *caches, size_t batch,
+                                      const spissa_kv_attention_config *cfg, float *d_out);
+
 /* Launch geometry of one attention call as the call itself computes it, on
  * the host, with no device work. No reference counterpart: it lets a caller
  * size workspaces before capturing a graph, and lets tests check the host
@@ -248,9 +263,11 @@ typedef struct {
 } spissa_attention_plan;
 /* past_lens[b]: cached tokens of sequence b, batch >= 1 (batch > 1 only with
  * query_len == 1); compute_units <= 0 means 256; prefill_precision as
- * spissa_session_set_prefill_precision. */
+ * spissa_session_set_prefill_precision; noalloc != 0 plans
+ * spissa_decode_step_device_noalloc (SHAPE when it would reject the call). */
 int spissa_plan_attention(const spissa_kv_attention_config *cfg, const size_t *past_lens, size_t batch,
-                          int compute_units, int prefill_precision, spissa_attention_plan *out);
+                          int compute_units, int prefill_precision, int noalloc,
+                          spissa_attention_plan *out);
 
 /* ops.rs:237-291 scaled_dot_product_attention (cacheless MHA, f32). */
 int spissa_scaled_dot_product_attention(const float *q, size_t q_len, const float *k,

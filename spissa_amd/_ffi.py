@@ -163,9 +163,14 @@ SIGNATURES = {
         C.c_int,
         [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, C.POINTER(c_void_p), c_size,
          C.POINTER(AttnConfigC), c_void_p]),
+    "spissa_decode_step_device_noalloc": (
+        C.c_int,
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, C.POINTER(c_void_p), c_size,
+         C.POINTER(AttnConfigC), c_void_p]),
     "spissa_plan_attention": (
         C.c_int,
-        [C.POINTER(AttnConfigC), C.POINTER(c_size), c_size, C.c_int, C.c_int, C.POINTER(AttentionPlanC)]),
+        [C.POINTER(AttnConfigC), C.POINTER(c_size), c_size, C.c_int, C.c_int, C.c_int,
+         C.POINTER(AttentionPlanC)]),
     "spissa_scaled_dot_product_attention": (
         C.c_int,
         [c_float_p, c_size, c_float_p, c_size, c_float_p, c_size, c_size, c_size, c_size, C.c_int,

@@ -74,6 +74,33 @@ struct DevBuf {
   size_t bytes = 0;
 };
 
+// Decode partials of spissa_decode_step_device_noalloc: a static device
+// array, one copy per GPU, held until the process ends and shared by every
+// such call on that GPU (calls that overlap on one GPU race). Nothing in it
+// needs clearing: a split writes its whole entry before the merge reads it,
+// and the merge reads only the splits that ran. Host code takes its device
+// address from hipGetSymbolAddress (scratch_address) and never passes the
+// array's name to a kernel.
+constexpr size_t kScratchBytes = (size_t)8 << 20;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+static std::mutex g_scratch_mu;
+static std::vector<float *> g_scratch_addr;  // per device
+
+// The device address of `scratch` on `device`, which must be current; looked
+// up once per device.
+static int scratch_address(int device, float **out) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if ((int)g_scratch_addr.size() <= device) g_scratch_addr.resize(device + 1, nullptr);
+  if (!g_scratch_addr[device]) {
+    void *p = nullptr;
+    HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return set_err(SPISSA_ERR_DEVICE, "hipGetSymbolAddress gave no address for the scratch array");
+    g_scratch_addr[device] = (float *)p;
+  }
+  *out = g_scratch_addr[device];
+  return SPISSA_OK;
+}
 
 struct spissa_session {
   int device = 0;
@@ -87,6 +114,7 @@ struct spissa_session {
   DevBuf ppart;     // prefill key-split partials (O, then (m, l))
   DevBuf sub;       // attention sublayer intermediates (normed x, q, k, v, attention, projection)
   DevBuf amax;      // argmax partials
+  float *scratch = nullptr;  // this device's copy of `scratch` (kScratchBytes)
   int cus = 256;    // compute units of the device
   // Buffers replaced by larger ones. They stay allocated until the session
   // is destroyed, so a HIP graph captured before a workspace grew still
@@ -162,6 +190,7 @@ extern "C" int spissa_session_create(int device, void *stream, spissa_session **
   std::unique_ptr<spissa_session> s(new spissa_session());
   s->device = device;
   HIP_TRY(hipDeviceGetAttribute(&s->cus, hipDeviceAttributeMultiprocessorCount, device));
+  ST_TRY(scratch_address(device, &s->scratch));
   if (stream) {
     s->stream = (hipStream_t)stream;
   } else {
@@ -1220,8 +1249,33 @@ extern "C" int spissa_decode_step_device(spissa_session *s, const spissa_rope_ta
   GUARD_END
 }
 
+extern "C" int spissa_decode_step_device_noalloc(spissa_session *s, const spissa_rope_table *table,
+                                                 const float *d_q, const float *d_k, const float *d_v,
+                                                 spissa_kv_cache *const *caches, size_t batch,
+                                                 const spissa_kv_attention_config *cfg, float *d_out) {
+  GUARD_BEGIN
+  ST_TRY(validate_decode_step(s, table, caches, batch, cfg));
+  if (!s->scratch) return set_err(SPISSA_ERR_DEVICE, "the session has no scratch array");
+  // One split per (sequence, KV head, head block) must fit; run_decode
+  // coarsens the splits to the array otherwise.
+  const size_t B = std::min<size_t>(batch, kMaxDecodeBatch);
+  const size_t single = B * cfg->num_heads * (cfg->head_dim + 2) * sizeof(float);
+  if (single > kScratchBytes)
+    return set_err(SPISSA_ERR_SHAPE,
+                   "decode partials of %zu sequences x %zu heads x head_dim %zu need %zu bytes; the scratch array "
+                   "holds %zu",
+                   B, cfg->num_heads, cfg->head_dim, single, kScratchBytes);
+  if (batch == 0) return SPISSA_OK;
+  HIP_TRY(hipSetDevice(s->device));
+  ST_TRY(run_decode(s, d_q, d_k, d_v, caches, batch, cfg, d_out, table, true, s->scratch, kScratchBytes));
+  for (size_t b = 0; b < batch; ++b) caches[b]->len += 1;
+  return SPISSA_OK;
+  GUARD_END
+}
+
 extern "C" int spissa_plan_attention(const spissa_kv_attention_config *cfg, const size_t *past_lens, size_t batch,
-                                     int compute_units, int prefill_precision, spissa_attention_plan *out) {
+                                     int compute_units, int prefill_precision, int noalloc,
+                                     spissa_attention_plan *out) {
   GUARD_BEGIN
   if (!cfg || !past_lens || !out) return set_err(SPISSA_ERR_ARGUMENT, "null argument");
   if (batch == 0) return set_err(SPISSA_ERR_ARGUMENT, "a plan needs at least one sequence");
@@ -1236,12 +1290,16 @@ extern "C" int spissa_plan_attention(const spissa_kv_attention_config *cfg, cons
   const int cus = compute_units > 0 ? compute_units : 256;
   if (cfg->query_len == 1 && decode_supported(D, Hq / Hkv)) {
     out->path = SPISSA_KERNEL_DECODE;
+    const size_t first = std::min<size_t>(batch, kMaxDecodeBatch);
+    if (noalloc && first * cfg->num_heads * (cfg->head_dim + 2) * sizeof(float) > kScratchBytes)
+      return set_err(SPISSA_ERR_SHAPE, "decode partials exceed the scratch array (%zu bytes)", kScratchBytes);
     for (size_t b0 = 0; b0 < batch; b0 += kMaxDecodeBatch) {
       const int B = (int)std::min<size_t>(kMaxDecodeBatch, batch - b0);
       int past[kMaxDecodeBatch];
       for (int b = 0; b < B; ++b) past[b] = (int)past_lens[b0 + b];
       DecodePlan p;
-      plan_decode(D, Hq, Hkv, cfg->window, past, B, 0, &p);
+      if (!plan_decode(D, Hq, Hkv, cfg->window, past, B, noalloc ? kScratchBytes : 0, &p))
+        return set_err(SPISSA_ERR_SHAPE, "decode partials exceed the scratch array (%zu bytes)", kScratchBytes);
       if (b0 == 0) {
         out->heads_per_block = p.RB;
         out->head_blocks = p.HB;

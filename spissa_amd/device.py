@@ -42,7 +42,7 @@ def _dev_i32(t, name: str) -> int:
 
 
 def plan_attention(config: KvAttentionConfig, past_lens: Sequence[int], compute_units: int = 256,
-                   precision: int = _ffi.PREFILL_BF16) -> dict:
+                   precision: int = _ffi.PREFILL_BF16, noalloc: bool = False) -> dict:
     """The launch geometry spissa_plan_attention reports for one attention call
     (no device needed): kernel path, decode head blocks and key splits, prefill
     tiles and key splits, grid and workspace bytes."""
@@ -51,7 +51,7 @@ def plan_attention(config: KvAttentionConfig, past_lens: Sequence[int], compute_
     cfg = config._c()
     plan = _ffi.AttentionPlanC()
     check(lib.spissa_plan_attention(C.byref(cfg), past, len(past_lens), compute_units, precision,
-                                    C.byref(plan)))
+                                    1 if noalloc else 0, C.byref(plan)))
     return {name: getattr(plan, name) for name, _ in _ffi.AttentionPlanC._fields_}
 
 
@@ -223,6 +223,18 @@ class Session:
             arr[i] = c.handle.value
         cfg = config._c()
         check(self._lib.spissa_decode_step_device(
+            self.handle, None if table is None else table.handle, _dev(q, "q"), _dev(k, "k"),
+            _dev(v, "v"), arr, len(caches), C.byref(cfg), _dev(out, "out")))
+
+    def decode_step_noalloc(self, table: Optional[RopeTable], q, k, v, caches: Sequence[KvCache],
+                            config: KvAttentionConfig, out) -> None:
+        """decode_step through spissa_decode_step_device_noalloc: no device allocation; the
+        partials live in the library's static per-GPU scratch array."""
+        arr = (_ffi.c_void_p * max(1, len(caches)))()
+        for i, c in enumerate(caches):
+            arr[i] = c.handle.value
+        cfg = config._c()
+        check(self._lib.spissa_decode_step_device_noalloc(
             self.handle, None if table is None else table.handle, _dev(q, "q"), _dev(k, "k"),
             _dev(v, "v"), arr, len(caches), C.byref(cfg), _dev(out, "out")))
 

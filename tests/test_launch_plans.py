@@ -18,14 +18,16 @@ import pytest
 
 from spissa_amd import _ffi
 from spissa_amd.device import plan_attention
+from spissa_amd.errors import ShapeError
 from spissa_amd.rotary import KvAttentionConfig
 
 MAX_DECODE_BATCH = 16
 MAX_DECODE_SPLITS = 512
+SCRATCH_BYTES = 8 << 20
 TILE_ALIGN = 64
 
 
-def check_decode(cfg, past, plan):
+def check_decode(cfg, past, plan, noalloc=False):
     """decode_split_kernel: grid (Hkv*HB, max_splits, B); split s of sequence b
     covers cached keys [kstart + s*kps, min(P, kstart + (s+1)*kps)) where
     kstart = max(0, P + 1 - W) with a window; the new token is the combine's."""
@@ -40,6 +42,8 @@ def check_decode(cfg, past, plan):
     assert plan["workgroups"] == B * Hkv * HB * max_splits
     groups = B * Hkv * HB
     assert plan["partial_bytes"] >= groups * max(1, max_splits) * entry * 4
+    if noalloc:
+        assert plan["partial_bytes"] <= SCRATCH_BYTES
     for b in range(B):
         P = past[b]
         kstart = max(0, P + 1 - W) if W > 0 else 0
@@ -140,15 +144,34 @@ BASELINE_PREFILL = [  # (name, S, P, Hq, Hkv, D, window, causal)
 
 
 @pytest.mark.parametrize("name,Hq,Hkv,D,past,W", BASELINE_DECODE, ids=[c[0] for c in BASELINE_DECODE])
-def test_decode_plan_covers_every_key(name, Hq, Hkv, D, past, W):
+@pytest.mark.parametrize("noalloc", [False, True])
+def test_decode_plan_covers_every_key(name, Hq, Hkv, D, past, W, noalloc):
     cfg = KvAttentionConfig(1, Hq, Hkv, D, True, W)
-    plan = plan_attention(cfg, past)
+    plan = plan_attention(cfg, past, noalloc=noalloc)
     for b0 in range(0, len(past), MAX_DECODE_BATCH):  # each launch of <= 16 sequences
         chunk = past[b0:b0 + MAX_DECODE_BATCH]
-        check_decode(cfg, chunk, plan_attention(cfg, chunk))
+        check_decode(cfg, chunk, plan_attention(cfg, chunk, noalloc=noalloc), noalloc)
     assert plan["partial_bytes"] >= max(
-        plan_attention(cfg, past[b0:b0 + MAX_DECODE_BATCH])["partial_bytes"]
+        plan_attention(cfg, past[b0:b0 + MAX_DECODE_BATCH], noalloc=noalloc)["partial_bytes"]
         for b0 in range(0, len(past), MAX_DECODE_BATCH))
+
+
+def test_noalloc_plan_coarsens_splits_to_the_scratch_array():
+    cfg = KvAttentionConfig(1, 32, 8, 256, True, 0)
+    past = [16384] + [64] * 15
+    wide = plan_attention(cfg, past)
+    narrow = plan_attention(cfg, past, noalloc=True)
+    assert wide["partial_bytes"] > SCRATCH_BYTES >= narrow["partial_bytes"]
+    assert narrow["splits"] < wide["splits"]
+    check_decode(cfg, past, narrow, noalloc=True)
+
+
+def test_noalloc_plan_rejects_partials_beyond_the_scratch_array():
+    # 16 sequences x 512 heads x (256 + 2) floats = 8.45 MB > 8 MiB even unsplit
+    cfg = KvAttentionConfig(1, 512, 512, 256, True, 0)
+    with pytest.raises(ShapeError):
+        plan_attention(cfg, [4] * 16, noalloc=True)
+    plan_attention(cfg, [4] * 15, noalloc=True)  # 7.9 MB fits
 
 
 @pytest.mark.parametrize("name,S,P,Hq,Hkv,D,W,causal", BASELINE_PREFILL, ids=[c[0] for c in BASELINE_PREFILL])
@@ -182,7 +205,8 @@ def test_decode_plan_sweep():
         past = [rng.choice([0, 1, 47, 512, 8191, 32768]) for _ in range(B)]
         W = rng.choice([0, 0, 1, 100, 1024])
         cfg = KvAttentionConfig(1, Hq, Hkv, D, True, W)
-        check_decode(cfg, past, plan_attention(cfg, past))
+        for noalloc in (False, True):
+            check_decode(cfg, past, plan_attention(cfg, past, noalloc=noalloc), noalloc)
 
 
 def test_plan_paths():
