@@ -269,6 +269,35 @@ int spissa_plan_attention(const spissa_kv_attention_config *cfg, const size_t *p
                           int compute_units, int prefill_precision, int noalloc,
                           spissa_attention_plan *out);
 
+/* One fused prefill (or chunked-prefill) step of one layer on the device,
+ * the call sequence of models/llama/generate.rs:383-416 for a chunk of
+ * cfg->query_len tokens: the RoPE of q and k at positions cache_len.. from
+ * `table` (rotary.rs:75-125 or 137-186, bit-identical to the drop-in RoPE;
+ * NULL: none), the attention of rotary.rs:335-415 over the cache's rows and
+ * the chunk, and KvCache::append of the rotated keys and the values
+ * (rotary.rs:226-256). In two launches: one pass appends the chunk to the
+ * cache (f32 rows and the bf16 prefill operands) and stages q, then the bf16
+ * MFMA attention reads every key from the cache. d_q, d_k, d_v are read-only;
+ * the cache gains query_len rows. All checks run before any launch; a device
+ * error (invalid softmax denominator) is reported by the next
+ * spissa_session_sync(), after the rows were appended (truncate rolls them
+ * back). head_dim 64, 128 or 256 with the bf16 prefill (SHAPE otherwise);
+ * query_len == 1 runs the fused decode step. */
+int spissa_prefill_step_device(spissa_session *s, const spissa_rope_table *table, const float *d_q,
+                               const float *d_k, const float *d_v, spissa_kv_cache *cache,
+                               const spissa_kv_attention_config *cfg, float *d_out);
+
+/* The attention of rotary.rs:335-415 in append-first order: the chunk's keys
+ * and values are already the cache's last cfg->query_len rows (appended
+ * before the call), so d_q [S, Hq, D] (rotated) attends over cache rows
+ * [0, len) with query i at absolute position len - S + i. Same result as
+ * spissa_attention_device(q, k, v, cache truncated to len - S, cfg) with the
+ * chunk's k/v passed as current rows; this is the fused prefill step's
+ * attention launch on its own. query_len > 1, bf16 prefill at head_dim 64,
+ * 128 or 256 (SHAPE otherwise); len >= query_len. */
+int spissa_attention_cached_device(spissa_session *s, const float *d_q, spissa_kv_cache *cache,
+                                   const spissa_kv_attention_config *cfg, float *d_out);
+
 /* ops.rs:237-291 scaled_dot_product_attention (cacheless MHA, f32). */
 int spissa_scaled_dot_product_attention(const float *q, size_t q_len, const float *k,
                                         size_t k_len, const float *v, size_t v_len,
@@ -378,6 +407,14 @@ typedef struct {
 int spissa_attention_sublayer_device(spissa_session *s, const spissa_attention_layer *layer,
                                      const float *d_x, size_t seq_len, spissa_kv_cache *cache,
                                      float *d_out);
+
+/* Streaming-read ceiling (no reference counterpart): reads the `bytes` bytes
+ * of d_buf once with 16-byte non-temporal loads, as the decode kernels read
+ * the cache, asynchronously on the session stream; timing a run of these
+ * gives the achievable read bandwidth the decode figures are compared with.
+ * d_buf 16-byte aligned, bytes a multiple of 16 (SHAPE otherwise); d_sink is
+ * one float the kernel may write. */
+int spissa_hbm_read_probe_device(spissa_session *s, const void *d_buf, size_t bytes, float *d_sink);
 
 /* Prefill arithmetic for query_len > 1: SPISSA_PREFILL_BF16 (default) runs
  * the MFMA kernel; SPISSA_PREFILL_F32 runs the f32 SIMT kernel. */

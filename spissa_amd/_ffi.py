@@ -171,6 +171,11 @@ SIGNATURES = {
         C.c_int,
         [C.POINTER(AttnConfigC), C.POINTER(c_size), c_size, C.c_int, C.c_int, C.c_int,
          C.POINTER(AttentionPlanC)]),
+    "spissa_hbm_read_probe_device": (C.c_int, [c_void_p, c_void_p, c_size, c_void_p]),
+    "spissa_prefill_step_device": (
+        C.c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, C.POINTER(AttnConfigC), c_void_p]),
+    "spissa_attention_cached_device": (
+        C.c_int, [c_void_p, c_void_p, c_void_p, C.POINTER(AttnConfigC), c_void_p]),
     "spissa_scaled_dot_product_attention": (
         C.c_int,
         [c_float_p, c_size, c_float_p, c_size, c_float_p, c_size, c_size, c_size, c_size, C.c_int,

@@ -114,6 +114,7 @@ struct spissa_session {
   DevBuf ppart;     // prefill key-split partials (O, then (m, l))
   DevBuf sub;       // attention sublayer intermediates (normed x, q, k, v, attention, projection)
   DevBuf amax;      // argmax partials
+  DevBuf qstage;    // fused prefill step: bf16 Q operand
   float *scratch = nullptr;  // this device's copy of `scratch` (kScratchBytes)
   int cus = 256;    // compute units of the device
   // Buffers replaced by larger ones. They stay allocated until the session
@@ -215,6 +216,7 @@ static void session_free(spissa_session *s) {
   free_buf(s->ppart);
   free_buf(s->sub);
   free_buf(s->amax);
+  free_buf(s->qstage);
   for (void *p : s->retired) (void)hipFree(p);
   if (s->d_err) (void)hipFree(s->d_err);
   if (s->own_stream) (void)hipStreamDestroy(s->stream);
@@ -276,6 +278,17 @@ extern "C" int spissa_session_sync(spissa_session *s) {
 
 extern "C" void *spissa_session_stream(spissa_session *s) { return s ? (void *)s->stream : nullptr; }
 extern "C" int spissa_session_device(const spissa_session *s) { return s ? s->device : -1; }
+
+extern "C" int spissa_hbm_read_probe_device(spissa_session *s, const void *d_buf, size_t bytes, float *d_sink) {
+  GUARD_BEGIN
+  if (!s || !d_buf || !d_sink) return set_err(SPISSA_ERR_ARGUMENT, "null argument");
+  if (bytes % 16 != 0 || reinterpret_cast<uintptr_t>(d_buf) % 16 != 0)
+    return set_err(SPISSA_ERR_SHAPE, "the read probe needs a 16-byte aligned buffer of a multiple of 16 bytes");
+  HIP_TRY(hipSetDevice(s->device));
+  HIP_TRY(launch_hbm_read(s->stream, d_buf, bytes, d_sink));
+  return SPISSA_OK;
+  GUARD_END
+}
 
 extern "C" int spissa_session_set_prefill_precision(spissa_session *s, int precision) {
   if (!s) return set_err(SPISSA_ERR_ARGUMENT, "session is null");
@@ -1270,6 +1283,121 @@ extern "C" int spissa_decode_step_device_noalloc(spissa_session *s, const spissa
   ST_TRY(run_decode(s, d_q, d_k, d_v, caches, batch, cfg, d_out, table, true, s->scratch, kScratchBytes));
   for (size_t b = 0; b < batch; ++b) caches[b]->len += 1;
   return SPISSA_OK;
+  GUARD_END
+}
+
+// The prefill over a chunk whose rows are already the cache's rows
+// [P, P + S): every key comes from the cache's bf16 shadow, so P8 covers the
+// whole padded key range and no staging buffer is used.
+static void plan_prefill_from_shadow(spissa_session *s, const spissa_kv_attention_config *cfg, size_t P,
+                                     PrefillArgs &a, PrefillPlan &plan) {
+  prefill_args_base(a, cfg, (int)P);
+  plan_prefill(a, (int)cfg->head_dim, s->cus, &plan);
+  a.P8 = (int)((P + cfg->query_len + 63) & ~(size_t)63);
+  a.cap_stage = 0;
+  plan.P8 = a.P8;
+  plan.cap_stage = 0;
+  plan.stage_bytes = 0;
+}
+
+// Launches the planned prefill (and its split combine) over the cache's
+// shadow, with Q from q (f32) or, when set, qb (scaled bf16).
+static int launch_prefill_from_shadow(spissa_session *s, PrefillArgs &a, const spissa_kv_cache *cache, const float *q,
+                                      const bf16 *qb, float *out, int D) {
+  a.q = q;
+  a.qb = qb;
+  a.out = out;
+  a.kb_cache = cache->kb;
+  a.vt_cache = cache->vt;
+  a.cap_cache = (long)cache->shadow_cap;
+  a.err = s->d_err;
+  if (a.splits > 1) {
+    const size_t rows = (size_t)a.splits * a.S * a.Hq;
+    a.part_o = (float *)s->ppart.p;
+    a.part_ml = a.part_o + rows * D;
+  }
+  HIP_TRY(launch_prefill(s->stream, a, D));
+  HIP_TRY(launch_prefill_combine(s->stream, a, D));
+  return SPISSA_OK;
+}
+
+extern "C" int spissa_prefill_step_device(spissa_session *s, const spissa_rope_table *table, const float *d_q,
+                                          const float *d_k, const float *d_v, spissa_kv_cache *cache,
+                                          const spissa_kv_attention_config *cfg, float *d_out) {
+  GUARD_BEGIN
+  if (!s || !cfg || !cache) return set_err(SPISSA_ERR_ARGUMENT, "null argument");
+  if (cfg->query_len == 1) return spissa_decode_step_device(s, table, d_q, d_k, d_v, &cache, 1, cfg, d_out);
+  ST_TRY(validate_attention(0, 0, 0, cache, cfg, false));
+  size_t n, nl;  // rotary.rs:227-251: the append must fit before anything runs
+  ST_TRY(kv_validate_append(cache, 0, 0, cfg->query_len, false, &n, &nl));
+  if (cache->session->device != s->device)
+    return set_err(SPISSA_ERR_ARGUMENT, "cache lives on device %d, session on %d", cache->session->device, s->device);
+  const int D = (int)cfg->head_dim;
+  if (!prefill_supported(D) || s->prefill_precision != SPISSA_PREFILL_BF16)
+    return set_err(SPISSA_ERR_SHAPE, "the fused prefill step runs the bf16 prefill at head_dim 64, 128 or 256, got %d",
+                   D);
+  const size_t P = cache->len, S = cfg->query_len;
+  if (table) {
+    if (table->kind == SPISSA_ROPE_NEOX || table->rotary_dim != cfg->head_dim)
+      return set_err(SPISSA_ERR_SHAPE, "the fused prefill step needs a llama or gemma table over the whole head");
+    if (P + S > table->max_positions)
+      return set_err(SPISSA_ERR_SHAPE, "positions up to %zu exceed the rope table (%zu positions)", P + S,
+                     table->max_positions);
+  }
+  if (!d_q || !d_k || !d_v || !d_out) return set_err(SPISSA_ERR_ARGUMENT, "null buffer");
+  HIP_TRY(hipSetDevice(s->device));
+  PrefillArgs a;
+  PrefillPlan plan;
+  plan_prefill_from_shadow(s, cfg, P, a, plan);
+  ST_TRY(ensure_shadow(cache, s->stream));
+  ST_TRY(ensure_buf(s, s->qstage, S * cfg->num_heads * cfg->head_dim * sizeof(bf16)));
+  if (plan.ppart_bytes) ST_TRY(ensure_buf(s, s->ppart, plan.ppart_bytes));
+  bf16 *qb = (bf16 *)s->qstage.p;
+  HIP_TRY(launch_prefill_append(s->stream, d_q, d_k, d_v, table ? table->cos : nullptr, table ? table->sin : nullptr,
+                                P, S, cfg->kv_heads, cfg->num_heads, cfg->head_dim, cache->keys, cache->values,
+                                cache->kb, cache->vt, cache->shadow_cap, qb, a.qk_scale_log2));
+  ST_TRY(launch_prefill_from_shadow(s, a, cache, d_q, qb, d_out, D));
+  cache->len = nl;
+  return SPISSA_OK;
+  GUARD_END
+}
+
+extern "C" int spissa_attention_cached_device(spissa_session *s, const float *d_q, spissa_kv_cache *cache,
+                                              const spissa_kv_attention_config *cfg, float *d_out) {
+  GUARD_BEGIN
+  if (!s || !cfg || !cache) return set_err(SPISSA_ERR_ARGUMENT, "null argument");
+  if (cfg->query_len < 2)
+    return set_err(SPISSA_ERR_SHAPE, "append-first attention needs query_len > 1, got %zu", cfg->query_len);
+  if (cache->len < cfg->query_len)
+    return set_err(SPISSA_ERR_SHAPE, "the cache holds %zu rows, fewer than the chunk's %zu", cache->len,
+                   cfg->query_len);
+  const size_t P = cache->len - cfg->query_len, S = cfg->query_len;
+  // rotary.rs:483-547 on the call as it would be made before the append
+  {
+    spissa_kv_cache before = *cache;
+    before.len = P;
+    ST_TRY(validate_attention(0, 0, 0, &before, cfg, false));
+  }
+  if (cache->session->device != s->device)
+    return set_err(SPISSA_ERR_ARGUMENT, "cache lives on device %d, session on %d", cache->session->device, s->device);
+  const int D = (int)cfg->head_dim;
+  if (!prefill_supported(D) || s->prefill_precision != SPISSA_PREFILL_BF16)
+    return set_err(SPISSA_ERR_SHAPE, "append-first attention runs the bf16 prefill at head_dim 64, 128 or 256, got %d",
+                   D);
+  if (!d_q || !d_out) return set_err(SPISSA_ERR_ARGUMENT, "null buffer");
+  HIP_TRY(hipSetDevice(s->device));
+  PrefillArgs a;
+  PrefillPlan plan;
+  plan_prefill_from_shadow(s, cfg, P, a, plan);
+  ST_TRY(ensure_shadow(cache, s->stream));
+  if (plan.ppart_bytes) ST_TRY(ensure_buf(s, s->ppart, plan.ppart_bytes));
+  // The last key tile reads shadow rows up to the next multiple of 64: they
+  // must hold finite values (zeros), whatever earlier, longer contents left.
+  const size_t pad_end = (P + S + 63) & ~(size_t)63;
+  if (pad_end > P + S)
+    HIP_TRY(launch_stage_bf16(s->stream, nullptr, nullptr, 0, pad_end - (P + S), cache->num_heads, cache->head_dim,
+                              cache->kb, cache->vt, P + S, cache->shadow_cap));
+  return launch_prefill_from_shadow(s, a, cache, d_q, nullptr, d_out, D);
   GUARD_END
 }
 

@@ -81,6 +81,9 @@ enum { kLinearGemv = 0, kLinearGemm = 1, kLinearGeneric = 2, kLinearSkinny = 3 }
 
 struct PrefillArgs {
   const float *q;     // [S, Hq, D] f32
+  // Or, when set, Q already scaled by qk_scale_log2 and rounded to bf16
+  // [S, Hq, D] (the fused prefill step's staging); q is then unused.
+  const bf16 *qb;
   float *out;         // [S, Hq, D] f32
   // bf16 K/V for keys [0, P8) come from the cache shadow, keys [P8, P+S) from
   // the staging buffer; P8 is a multiple of kPrefillTileAlign, so no key tile
@@ -143,11 +146,21 @@ hipError_t launch_gemma_prologue(hipStream_t st, const float *cos_tab, const flo
                                  size_t tab_stride, float *q, float *k, size_t S, size_t qh,
                                  size_t kh, size_t D, size_t half, const float *qn,
                                  const float *kn, float eps, float prescale);
+// The append half of a fused prefill step: rows [0, S) of k/v (optionally
+// rotated with cos/sin rows at positions P + i) into cache rows [P, P + S)
+// and the bf16 shadow (zeros up to the next multiple of 64), and q rotated,
+// scaled by qscale and rounded into qb [S, Hq, D] bf16. D % 64 == 0.
+hipError_t launch_prefill_append(hipStream_t st, const float *q, const float *k, const float *v,
+                                 const float *cos_tab, const float *sin_tab, size_t P, size_t S, size_t H,
+                                 size_t Hq, size_t D, float *cache_k, float *cache_v, bf16 *kb, bf16 *vt,
+                                 size_t cap, bf16 *qb, float qscale);
 // Writes rows [0, n) and zero rows [n, n_pad) at buffer positions dst_first + i.
 hipError_t launch_stage_bf16(hipStream_t st, const float *k_rows, const float *v_rows, size_t n,
                              size_t n_pad, size_t H, size_t D, bf16 *kb, bf16 *vt,
                              size_t dst_first, size_t dst_cap);
 hipError_t launch_decode(hipStream_t st, const DecodeArgs &a, int D, int RB);
+// Streaming-read probe: reads bytes (a multiple of 16, 16-byte aligned) of buf once.
+hipError_t launch_hbm_read(hipStream_t st, const void *buf, size_t bytes, float *sink);
 hipError_t launch_prefill(hipStream_t st, const PrefillArgs &a, int D);
 // Merges the key splits of a split prefill into `out` (and the error flag).
 hipError_t launch_prefill_combine(hipStream_t st, const PrefillArgs &a, int D);

@@ -238,6 +238,12 @@ prefill_kernel(const PrefillArgs a) {
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     const int pos = min(wp0 + 32 * qb + lq, a.S - 1);
+    if (a.qb) {  // already scaled and rounded (the fused prefill step)
+      const bf16 *qp = a.qb + ((long)pos * a.Hq + head) * D + 8 * hl;
+#pragma unroll
+      for (int t = 0; t < DT; ++t) qf[qb][t] = *reinterpret_cast<const bf16x8 *>(qp + 16 * t);
+      continue;
+    }
     const float *qp = a.q + ((long)pos * a.Hq + head) * D + 8 * hl;
 #pragma unroll
     for (int t = 0; t < DT; ++t) {

@@ -6,6 +6,8 @@
 // pair) formula and glibc libm, every multiply and add is rounded separately
 // (contraction off), and hipcc's default f32 division and sqrt are correctly
 // rounded.
+#include <algorithm>
+
 #include "internal.hpp"
 
 namespace spissa {
@@ -240,7 +242,154 @@ __global__ __launch_bounds__(256) void stage_bf16_kernel(const float *__restrict
   }
 }
 
+// The append and operand staging of a fused prefill step, in one pass over
+// the chunk's rows: the RoPE of rotary.rs:75-125 / 137-186 (optional, table
+// rows are absolute positions), then KvCache::append (rotary.rs:226-256).
+//   K/V blocks (blockIdx.y < H): cache position P + i receives row i of the
+//     chunk: the rotated key and the value in the f32 rows, the bf16 key in
+//     the shadow K [H, cap, D] and the bf16 value at slot vt_key_slot(pos) of
+//     the shadow V^T [H, D, cap]; shadow positions [P + S, pad_end) are zeroed
+//     so the last key tile the prefill kernel reads is finite.
+//   Q blocks (blockIdx.y >= H): query row i, rotated at position P + i,
+//     times qscale, rounded to bf16 into qb [S, Hq, D] -- the prefill
+//     kernel's Q operand, the same bits it would form from the rotated f32 row.
+// A block owns 64 positions and the 32 rotary pairs [32z, 32z + 32) of one
+// head, i.e. dims [32z, +32) and [D/2 + 32z, +32); thread t holds position
+// t / 4 and the eight pairs 8(t % 4) .. +7 of that range: a float4 pair of
+// each half. Values pass through an LDS tile for the V^T stores.
+// Grid: (position blocks, H + Hq, D / 64), 256 threads.
+__global__ __launch_bounds__(256) void prefill_append_kernel(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+    const float *__restrict__ cos_tab, const float *__restrict__ sin_tab, long P, long S, int H, int Hq, int D,
+    float *__restrict__ cache_k, float *__restrict__ cache_v, bf16 *__restrict__ kb, bf16 *__restrict__ vt,
+    long cap, long pad_end, bf16 *__restrict__ qb, float qscale) {
+#pragma clang fp contract(off)
+  typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+  __shared__ float tile[64][65];  // V[position][lo 32 | hi 32 dims], padded against bank conflicts
+  const int half = D / 2;
+  const int r = threadIdx.x >> 2, c = threadIdx.x & 3;
+  const int p0 = 32 * blockIdx.z + 8 * c;  // first pair of this thread
+  const bool kv = (int)blockIdx.y < H;
+
+  auto rotate = [&](float4 (&lo)[2], float4 (&hi)[2], long pos) {
+    if (!cos_tab) return;
+    const float *cp = cos_tab + pos * half + p0, *sp = sin_tab + pos * half + p0;
+    float *a = reinterpret_cast<float *>(lo), *b = reinterpret_cast<float *>(hi);
+    float cs[8], sn[8];
+    *reinterpret_cast<float4 *>(cs) = *reinterpret_cast<const float4 *>(cp);
+    *reinterpret_cast<float4 *>(cs + 4) = *reinterpret_cast<const float4 *>(cp + 4);
+    *reinterpret_cast<float4 *>(sn) = *reinterpret_cast<const float4 *>(sp);
+    *reinterpret_cast<float4 *>(sn + 4) = *reinterpret_cast<const float4 *>(sp + 4);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {  // rotate_neox_pair (rotary.rs:467-481)
+      const float first = a[j], second = b[j];
+      a[j] = first * cs[j] - second * sn[j];
+      b[j] = second * cs[j] + first * sn[j];
+    }
+  };
+  auto to_bf16 = [](const float4 (&x)[2], float s) {
+    const float *f = reinterpret_cast<const float *>(x);
+    bf16x8 o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = (bf16)(f[j] * s);
+    return o;
+  };
+  auto load2 = [](const float *p, float4 (&x)[2]) {
+    x[0] = *reinterpret_cast<const float4 *>(p);
+    x[1] = *reinterpret_cast<const float4 *>(p + 4);
+  };
+  auto store2 = [](float *p, const float4 (&x)[2]) {
+    *reinterpret_cast<float4 *>(p) = x[0];
+    *reinterpret_cast<float4 *>(p + 4) = x[1];
+  };
+
+  if (!kv) {
+    const int hq = blockIdx.y - H;
+    const long i = 64L * blockIdx.x + r;
+    if (i >= S) return;
+    const float *src = q + (i * Hq + hq) * (long)D;
+    float4 lo[2], hi[2];
+    load2(src + p0, lo);
+    load2(src + half + p0, hi);
+    rotate(lo, hi, P + i);
+    bf16 *dst = qb + (i * Hq + hq) * (long)D;
+    *reinterpret_cast<bf16x8 *>(dst + p0) = to_bf16(lo, qscale);
+    *reinterpret_cast<bf16x8 *>(dst + half + p0) = to_bf16(hi, qscale);
+    return;
+  }
+
+  const int h = blockIdx.y;
+  const long P0 = (P & ~63L) + 64L * blockIdx.x;
+  const long pos = P0 + r;
+  float4 klo[2], khi[2], vlo[2], vhi[2];
+  const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+  klo[0] = klo[1] = khi[0] = khi[1] = vlo[0] = vlo[1] = vhi[0] = vhi[1] = z;
+  const bool row = pos >= P && pos < P + S;
+  if (row) {
+    const long i = pos - P;
+    const float *ks = k + (i * H + h) * (long)D, *vs = v + (i * H + h) * (long)D;
+    load2(ks + p0, klo);
+    load2(ks + half + p0, khi);
+    load2(vs + p0, vlo);
+    load2(vs + half + p0, vhi);
+    rotate(klo, khi, pos);
+    float *ck = cache_k + (pos * H + h) * (long)D, *cv = cache_v + (pos * H + h) * (long)D;
+    store2(ck + p0, klo);
+    store2(ck + half + p0, khi);
+    store2(cv + p0, vlo);
+    store2(cv + half + p0, vhi);
+  }
+  if (pos >= P && pos < pad_end) {  // the chunk's rows, then zero padding
+    bf16 *dk = kb + ((long)h * cap + pos) * D;
+    *reinterpret_cast<bf16x8 *>(dk + p0) = to_bf16(klo, 1.0f);
+    *reinterpret_cast<bf16x8 *>(dk + half + p0) = to_bf16(khi, 1.0f);
+  }
+  {
+    float *t = &tile[r][8 * c];
+    const float *a = reinterpret_cast<const float *>(vlo), *b = reinterpret_cast<const float *>(vhi);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      t[j] = a[j];
+      t[32 + j] = b[j];
+    }
+  }
+  __syncthreads();
+  // V^T: 64 dim rows (lo 32, hi 32) x 64 slots, eight slots per store.
+  for (int w = threadIdx.x; w < 64 * 8; w += 256) {
+    const int dd = w >> 3, c8 = w & 7;
+    const int dim = dd < 32 ? 32 * blockIdx.z + dd : half + 32 * blockIdx.z + (dd - 32);
+    const long s0 = P0 + 8 * c8;
+    bf16 *dst = vt + ((long)h * D + dim) * cap;
+    const long g0 = s0 & ~15L;  // the aligned 16-key group these slots hold
+    if (g0 >= P && g0 + 16 <= pad_end) {
+      bf16x8 vv;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) vv[j] = (bf16)tile[vt_key_slot(s0 + j) - P0][dd];
+      *reinterpret_cast<bf16x8 *>(dst + s0) = vv;
+    } else {
+      for (int j = 0; j < 8; ++j) {
+        const long sl = s0 + j, key = vt_key_slot(sl);
+        if (key >= P && key < pad_end) dst[sl] = (bf16)tile[key - P0][dd];
+      }
+    }
+  }
+}
+
 static inline unsigned blocks_for(long n, int per) { return (unsigned)((n + per - 1) / per); }
+
+hipError_t launch_prefill_append(hipStream_t st, const float *q, const float *k, const float *v,
+                                 const float *cos_tab, const float *sin_tab, size_t P, size_t S, size_t H,
+                                 size_t Hq, size_t D, float *cache_k, float *cache_v, bf16 *kb, bf16 *vt,
+                                 size_t cap, bf16 *qb, float qscale) {
+  if (S == 0) return hipSuccess;
+  const long pad_end = ((long)(P + S) + 63) & ~63L;
+  if (D % 64 != 0 || cap % 64 != 0 || pad_end > (long)cap) return hipErrorInvalidValue;
+  const long kv_blocks = (pad_end - ((long)P & ~63L)) / 64, q_blocks = ((long)S + 63) / 64;
+  dim3 grid((unsigned)std::max(kv_blocks, q_blocks), (unsigned)(H + Hq), (unsigned)(D / 64));
+  hipLaunchKernelGGL(prefill_append_kernel, grid, dim3(256), 0, st, q, k, v, cos_tab, sin_tab, (long)P, (long)S,
+                     (int)H, (int)Hq, (int)D, cache_k, cache_v, kb, vt, (long)cap, pad_end, qb, qscale);
+  return hipGetLastError();
+}
 
 hipError_t launch_rope_apply(hipStream_t st, const float *cos_tab, const float *sin_tab,
                              size_t tab_stride, float *q, float *k, size_t S, size_t qh,

@@ -238,6 +238,31 @@ class Session:
             self.handle, None if table is None else table.handle, _dev(q, "q"), _dev(k, "k"),
             _dev(v, "v"), arr, len(caches), C.byref(cfg), _dev(out, "out")))
 
+    def prefill_step(self, table: Optional[RopeTable], q, k, v, cache: KvCache, config: KvAttentionConfig,
+                     out) -> None:
+        """Fused RoPE + attention + append of a chunk of config.query_len tokens
+        (spissa_prefill_step_device): q [S, Hq, D], k/v [S, Hkv, D] read-only;
+        the cache gains S rows holding the rotated keys and the values."""
+        cfg = config._c()
+        check(self._lib.spissa_prefill_step_device(
+            self.handle, None if table is None else table.handle, _dev(q, "q"), _dev(k, "k"), _dev(v, "v"),
+            cache.handle, C.byref(cfg), _dev(out, "out")))
+
+    def attention_cached(self, q, cache: KvCache, config: KvAttentionConfig, out) -> None:
+        """Append-first attention (spissa_attention_cached_device): the chunk's
+        rows are already the cache's last config.query_len rows."""
+        cfg = config._c()
+        check(self._lib.spissa_attention_cached_device(self.handle, _dev(q, "q"), cache.handle, C.byref(cfg),
+                                                       _dev(out, "out")))
+
+    def hbm_read_probe(self, buf, sink) -> None:
+        """Reads every byte of the device tensor `buf` once (the streaming-read
+        ceiling kernel); `sink` is a float32 device tensor of one element."""
+        if not getattr(buf, "is_cuda", False):
+            raise TypeError("buf must be a device tensor")
+        check(self._lib.spissa_hbm_read_probe_device(self.handle, buf.data_ptr(),
+                                                     buf.numel() * buf.element_size(), _dev(sink, "sink")))
+
     def append(self, cache: KvCache, k, v, token_count: int) -> None:
         cache.append_device(_dev(k, "k"), _dev(v, "v"), token_count)
 
