@@ -305,7 +305,10 @@ __global__ __launch_bounds__(256, 4) void decode_split_kernel(const DecodeArgs a
 // Finishes the attention of one (sequence, KV head, head block): the new
 // token's score and value, merged with the partials of every split of the
 // cached keys, then the optional append of the new key and value.
-// Grid: (RB*D / OUTS, Hkv*HB, B); 1024 threads = OUTS consecutive outputs x
+// Grid: (Hkv*HB, RB*D / OUTS, B), the head blocks fastest as in the split
+// kernel: consecutive workgroups go to consecutive XCDs, so the combine of a
+// head runs on the XCD whose workgroups wrote that head's partials (measured
+// 4% faster per batch-1 layer at 8192 keys). 1024 threads = OUTS consecutive outputs x
 // SL split lanes (64 x 16, or 16 x 64 when there are many splits). Each lane
 // keeps an online (max, sum, output) over its splits with the loads of eight
 // splits in flight; the SL lanes of every output are merged through LDS.
@@ -318,8 +321,8 @@ __global__ __launch_bounds__(1024) void decode_combine_kernel(const DecodeArgs a
   __shared__ float s_dot[RB * D / 64];
   __shared__ float s_new[RB];
 
-  const int hb = blockIdx.y % a.HB;
-  const int h = blockIdx.y / a.HB;
+  const int hb = blockIdx.x % a.HB;
+  const int h = blockIdx.x / a.HB;
   const int b = blockIdx.z;
   const int P = a.seq[b].past;
   const int kstart = a.window > 0 ? max(0, P + 1 - a.window) : 0;
@@ -327,7 +330,7 @@ __global__ __launch_bounds__(1024) void decode_combine_kernel(const DecodeArgs a
   const int tid = threadIdx.x;
   const int out = tid & (OUTS - 1);
   const int sl = tid / OUTS;
-  const int e = blockIdx.x * OUTS + out;  // < RB*D: RB*D is a multiple of OUTS
+  const int e = blockIdx.y * OUTS + out;  // < RB*D: RB*D is a multiple of OUTS
   const int r = e / D;
   const int qh0 = h * a.R + hb * RB;
   const float *knew = a.cur_k + ((long)b * a.Hkv + h) * D;
@@ -429,7 +432,7 @@ __global__ __launch_bounds__(1024) void decode_combine_kernel(const DecodeArgs a
     if ((e % D) == 0 && !(L > 0.0f && L < __builtin_inff())) atomicOr(a.err, kDevErrSoftmaxDenominator);
   }
   // ---- append the new (rotated) key and value at cache row P ----
-  if (a.do_append && blockIdx.x == 0 && hb == 0 && tid < D) {
+  if (a.do_append && blockIdx.y == 0 && hb == 0 && tid < D) {
     const float vd = vnew[tid];
     a.app_k[b][(long)h * D + tid] = kd;
     a.app_v[b][(long)h * D + tid] = vd;
@@ -459,10 +462,10 @@ hipError_t launch_one(hipStream_t st, const DecodeArgs &a) {
     if (e != hipSuccess) return e;
   }
   if (a.max_splits > kCombineWideSplits) {
-    dim3 cgrid((unsigned)(RB * D / 16), (unsigned)(a.Hkv * a.HB), (unsigned)a.B);
+    dim3 cgrid((unsigned)(a.Hkv * a.HB), (unsigned)(RB * D / 16), (unsigned)a.B);
     hipLaunchKernelGGL((decode_combine_kernel<D, RB, 64>), cgrid, dim3(1024), 0, st, a);
   } else {
-    dim3 cgrid((unsigned)(RB * D / 64), (unsigned)(a.Hkv * a.HB), (unsigned)a.B);
+    dim3 cgrid((unsigned)(a.Hkv * a.HB), (unsigned)(RB * D / 64), (unsigned)a.B);
     hipLaunchKernelGGL((decode_combine_kernel<D, RB, 16>), cgrid, dim3(1024), 0, st, a);
   }
   return hipGetLastError();
