@@ -162,6 +162,73 @@ __global__ void gemma_prologue_kernel(const float *__restrict__ cos_tab,
   }
 }
 
+// The same prologue with one wave per row, for D = 64, 128 or 256: lane l
+// holds elements [l * D/64, (l + 1) * D/64) of the row, so every load and
+// store is coalesced, and its rotate-half partners sit in lane l ^ 32. The
+// squares go through LDS and lane 0 adds them in index order, so the sum is
+// the reference's sequential one, bit for bit (ops.rs:159-179); the norm,
+// rotation and prescale then run on all lanes. Four rows per workgroup.
+template <int D>
+__global__ __launch_bounds__(256) void gemma_prologue_wave_kernel(
+    const float *__restrict__ cos_tab, const float *__restrict__ sin_tab, long tab_stride, float *__restrict__ q,
+    float *__restrict__ k, long S, int qh, int kh, const float *__restrict__ qn, const float *__restrict__ kn,
+    float eps, float prescale) {
+#pragma clang fp contract(off)
+  constexpr int E = D / 64, HALF = D / 2;
+  __shared__ float sq[4][D];
+  __shared__ float inv_s[4];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const long row = (long)blockIdx.x * 4 + wave;
+  const bool live = row < S * (qh + kh);
+  long pos = 0;
+  bool is_q = false;
+  float *x = nullptr;
+  const float *w = nullptr;
+  float v[E];
+  if (live) {
+    pos = row / (qh + kh);
+    const int hh = (int)(row - pos * (qh + kh));
+    is_q = hh < qh;
+    x = is_q ? q + (pos * qh + hh) * (long)D : k + (pos * kh + (hh - qh)) * (long)D;
+    w = is_q ? qn : kn;
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+      v[j] = x[lane * E + j];
+      sq[wave][lane * E + j] = v[j] * v[j];
+    }
+  }
+  __syncthreads();
+  if (live && lane == 0) {
+    float acc = 0.0f;
+    for (int c = 0; c < D; ++c) acc += sq[wave][c];
+    const float mean_square = acc / (float)D;
+    inv_s[wave] = 1.0f / sqrtf(mean_square + eps);
+  }
+  __syncthreads();
+  if (!live) return;
+  const float inv_rms = inv_s[wave];
+  float nv[E];
+#pragma unroll
+  for (int j = 0; j < E; ++j) nv[j] = v[j] * inv_rms * w[lane * E + j];
+  // rotate-half: lanes < 32 hold first halves (pairs p = lane*E + j), lanes
+  // >= 32 the second halves of the same pairs
+  const bool lo = lane < 32;
+  const int p0 = (lane & 31) * E;
+  const float *ct = cos_tab + pos * tab_stride + p0;
+  const float *st = sin_tab + pos * tab_stride + p0;
+#pragma unroll
+  for (int j = 0; j < E; ++j) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(nv[j]), __float_as_uint(nv[j]), false, false);
+    const float partner = __uint_as_float(lo ? r[1] : r[0]);
+    const float first = lo ? nv[j] : partner, second = lo ? partner : nv[j];
+    const float c = ct[j], s = st[j];
+    float o = lo ? first * c - second * s : second * c + first * s;
+    if (is_q) o *= prescale;
+    x[lane * E + j] = o;
+  }
+  static_assert(HALF == 32 * E, "rotate-half partners are 32 lanes apart");
+}
+
 // Converts n rows of K and V ([n, H, D] f32) to the prefill operand layouts:
 // kb [H, cap, D] bf16 (head-major K) and vt [H, D, cap] bf16 (transposed V,
 // key p stored at slot vt_key_slot(p)), at buffer positions dst_first + i.
@@ -426,6 +493,13 @@ hipError_t launch_gemma_prologue(hipStream_t st, const float *cos_tab, const flo
                                  const float *kn, float eps, float prescale) {
   long rows = (long)S * (long)(qh + kh);
   if (rows == 0) return hipSuccess;
+  if (2 * half == D && (D == 64 || D == 128 || D == 256)) {  // one wave per row, coalesced
+    auto kern = D == 64 ? gemma_prologue_wave_kernel<64>
+                : D == 128 ? gemma_prologue_wave_kernel<128> : gemma_prologue_wave_kernel<256>;
+    hipLaunchKernelGGL(kern, dim3(blocks_for(rows, 4)), dim3(256), 0, st, cos_tab, sin_tab, (long)tab_stride, q, k,
+                       (long)S, (int)qh, (int)kh, qn, kn, eps, prescale);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(gemma_prologue_kernel, dim3(blocks_for(rows, 64)), dim3(64), 0, st, cos_tab,
                      sin_tab, (long)tab_stride, q, k, (long)S, (int)qh, (int)kh, (int)D, (int)half,
                      qn, kn, eps, prescale);

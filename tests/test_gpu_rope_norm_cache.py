@@ -92,14 +92,20 @@ def test_rms_norm_bitwise(gpu, rows, cols):
     assert_bitwise(gpu.rms_norm(x, w, rows, cols, 1e-6), o.rms_norm(x, w, rows, cols, 1e-6), "rms_norm")
 
 
-@pytest.mark.parametrize("layer", [0, 5])
-def test_gemma_qk_prologue_device_bitwise(gpu, layer):
+@pytest.mark.parametrize("layer,S,Hq,Hkv,D", [
+    (0, 17, 8, 4, 256), (5, 17, 8, 4, 256),
+    (0, 5, 2, 1, 128),   # 15 rows: the last workgroup has one idle wave
+    (5, 9, 4, 1, 64),
+])
+def test_gemma_qk_prologue_device_bitwise(gpu, layer, S, Hq, Hkv, D):
+    """models/gemma/generate.rs:232-278 on the device (one wave per row, lane 0
+    summing the staged squares in index order) against the oracle, bitwise."""
     import torch
 
     from spissa_amd import _ffi
     from spissa_amd.device import Session
 
-    S, Hq, Hkv, D, off = 17, 8, 4, 256, 1000
+    off = 1000
     is_global = gpu.is_global_layer(layer, 6)
     base, div = (1e6, 8.0) if is_global else (10000.0, 1.0)
     q, k = normal_f32(seed_for(5, layer, 0, "q"), S * Hq * D), normal_f32(seed_for(5, layer, 0, "k"), S * Hkv * D)
