@@ -765,7 +765,10 @@ def configs_bench(sess, stream, gen, dev, args, time_graph) -> dict:
     from spissa_amd.rotary import KvAttentionConfig
 
     out = {}
+    only = set(args.configs.split(",")) if getattr(args, "configs", None) else None
     for name, cfg_id, L, hq, hkv, d, S, P, W, rope in CONFIG_CASES:
+        if only is not None and name not in only:
+            continue
         w = hkv * d
         with torch.cuda.stream(stream):
             caches = []
@@ -824,6 +827,34 @@ def configs_bench(sess, stream, gen, dev, args, time_graph) -> dict:
         del g, caches, q, k, v, o, table
         torch.cuda.empty_cache()
     return out
+
+
+def configs_only(args) -> dict:
+    """The records of the CONFIG_CASES named in --configs, nothing else."""
+    import torch
+
+    from spissa_amd.device import Session
+
+    torch.cuda.init()
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream()
+    sess = Session(0, stream=stream)
+    gen = torch.Generator(device=dev)
+
+    def time_graph(g, reps, warm):
+        for _ in range(warm):
+            g.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        sess.sync()
+        return a.elapsed_time(b) / reps
+
+    return configs_bench(sess, stream, gen, dev, args, time_graph)
 
 
 def cpu_model() -> str:
@@ -980,12 +1011,18 @@ def main() -> int:
     ap.add_argument("--decode-only", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a 256 MiB device copy (HBM-counter calibration under rocprofv3 --pmc)")
+    ap.add_argument("--configs", default="",
+                    help="only time these comma-separated cases of CONFIG_CASES and print their records "
+                         "(for counter passes); the benchmark line is not printed")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build's attention path has no multi-GPU leg "
               "(run with --gpus 1)", file=sys.stderr)
         return 2
 
+    if args.configs:
+        print(json.dumps(configs_only(args)), flush=True)
+        return 0
     t0 = time.time()
     res = gpu_bench(args)
     log(f"gpu part done in {time.time() - t0:.1f}s")
