@@ -527,14 +527,18 @@ GEMMA_WORKLOADS = {  # BASELINE configs 3 and 4: heads, head_dim, layers, local 
 def workloads_bench(sess, stream, gen, dev, args, time_graph) -> dict:
     """BASELINE configs 3 and 4 as whole workloads through every layer, in the
     reference's per-layer order (models/gemma/generate.rs:232-295): the QK-norm
-    + Gemma RoPE + prescale prologue of the layer's new q and k rows
-    (spissa_gemma_qk_prologue_device), then the fused step (attention over the
-    cache and the new rows, append). Local layers use the sliding window with
-    RoPE base 1e4; global layers ((l + 1) % 6 == 0) see every key, RoPE base 1e6
-    with position divisor 8. Each workload is one graph per phase set; the
-    phases are the reference's buckets (session.rs:14-32): rotary (the
-    prologue), attention and kv_append (the fused step's append pass, where it
-    is a launch of its own)."""
+    + Gemma RoPE + prescale prologue of the layer's new q and k rows, the
+    attention over the cache and the new rows, the append. Prefill chunks run
+    the prologue (spissa_gemma_qk_prologue_device) and then the fused prefill
+    step; a decode token runs spissa_gemma_decode_step_device, which does all
+    of it in two launches. Local layers use the sliding window with RoPE base
+    1e4; global layers ((l + 1) % 6 == 0) see every key, RoPE base 1e6 with
+    position divisor 8. Each workload is one graph per phase set; the phases
+    are the reference's buckets (session.rs:14-32): rotary (the prologue),
+    attention and kv_append (the fused step's append pass, where it is a
+    launch of its own). A decode token's buckets are timed on the unfused
+    sequence (prologue launch, then the decode step), which is also reported
+    whole beside the fused step."""
     import torch
 
     from spissa_amd import _ffi
@@ -630,10 +634,15 @@ def workloads_bench(sess, stream, gen, dev, args, time_graph) -> dict:
         for l in range(L):
             sess.decode_step(None, q[l], k[l], v[l], [caches[l]], dcfgs[l], o[l])
 
-    def d_layers():
+    def d_unfused():
         for l in range(L):
             sess.gemma_qk_prologue(tab[kinds[l]], q[l], k[l], 1, hq, hkv, d, qn[l], kn[l], 1e-6, P, 1.0)
             sess.decode_step(None, q[l], k[l], v[l], [caches[l]], dcfgs[l], o[l])
+
+    def d_layers():
+        for l in range(L):
+            sess.gemma_decode_step(tab[kinds[l]], q[l], k[l], v[l], [caches[l]], dcfgs[l], qn[l], kn[l], 1e-6, 1.0,
+                                   o[l])
 
     def reset():
         for c in caches:
@@ -642,15 +651,19 @@ def workloads_bench(sess, stream, gen, dev, args, time_graph) -> dict:
     d_steps()
     sess.sync()
     reset()
+    d_layers()
+    sess.sync()
+    reset()
     graphs = {}
-    for n, fn in (("all", d_layers), ("rotary", d_prologue), ("step", d_steps)):
+    for n, fn in (("all", d_layers), ("unfused", d_unfused), ("rotary", d_prologue), ("step", d_steps)):
         graphs[n] = captured(fn)
         reset()
     ms = {n: time_graph(g, max(5, args.steps), 3) for n, g in graphs.items()}
     rec["decode_32768"] = {"ms_per_token": round(ms["all"], 4), "tokens_per_s": round(1e3 / ms["all"], 1),
                            "us_per_layer": round(ms["all"] * 1e3 / L, 3),
-                           "phases_ms": {"rotary": round(ms["rotary"], 4),
-                                         "attention_and_kv_append": round(ms["step"], 4)}}
+                           "unfused_ms_per_token": round(ms["unfused"], 4),
+                           "unfused_phases_ms": {"rotary": round(ms["rotary"], 4),
+                                                 "attention_and_kv_append": round(ms["step"], 4)}}
     out["gemma3_1b"] = rec
     del graphs, caches, q, k, v, o
     torch.cuda.empty_cache()
@@ -689,6 +702,11 @@ def workloads_bench(sess, stream, gen, dev, args, time_graph) -> dict:
 
     def decode_token():
         for l in range(L):
+            sess.gemma_decode_step(tab[kinds[l]], q[l], k[l], v[l], [caches[l]], dcfg[l], qn[l], kn[l], 1e-6, 1.0,
+                                   o[l])
+
+    def decode_token_unfused():
+        for l in range(L):
             pos = caches[l].len()
             sess.gemma_qk_prologue(tab[kinds[l]], q[l], k[l], 1, hq, hkv, d, qn[l], kn[l], 1e-6, pos, 1.0)
             sess.decode_step(None, q[l], k[l], v[l], [caches[l]], dcfg[l], o[l])
@@ -711,6 +729,9 @@ def workloads_bench(sess, stream, gen, dev, args, time_graph) -> dict:
     g_tok = captured(decode_token)
     for c in caches:
         c.truncate(P + S)
+    g_tok_unf = captured(decode_token_unfused)
+    for c in caches:
+        c.truncate(P + S)
 
     def tok_prologue():
         for l in range(L):
@@ -726,6 +747,7 @@ def workloads_bench(sess, stream, gen, dev, args, time_graph) -> dict:
     ms_turn = time_graph(g_turn, 3, 1)
     ms_chunk = time_graph(g_chunk, reps, 2)
     ms_tok = time_graph(g_tok, max(5, args.steps), 3)
+    ms_unf = time_graph(g_tok_unf, max(5, args.steps), 3)
     ms_rot = time_graph(g_tok_rot, max(5, args.steps), 3)
     ms_st = time_graph(g_tok_step, max(5, args.steps), 3)
     decode_ms = ms_turn - ms_chunk
@@ -736,10 +758,11 @@ def workloads_bench(sess, stream, gen, dev, args, time_graph) -> dict:
                  "chunk_ms": round(ms_chunk, 3), "chunk_us_per_layer": round(ms_chunk * 1e3 / L, 2),
                  "decode_ms": round(decode_ms, 3), "decode_tokens_per_s": round(T / (decode_ms * 1e-3), 1)},
         "decode_token_after_chunk": {"ms": round(ms_tok, 4), "us_per_layer": round(ms_tok * 1e3 / L, 3),
-                                     "phases_ms": {"rotary": round(ms_rot, 4),
-                                                   "attention_and_kv_append": round(ms_st, 4)}},
+                                     "unfused_ms": round(ms_unf, 4),
+                                     "unfused_phases_ms": {"rotary": round(ms_rot, 4),
+                                                           "attention_and_kv_append": round(ms_st, 4)}},
     }
-    del g_turn, g_chunk, g_tok, g_tok_rot, g_tok_step, caches
+    del g_turn, g_chunk, g_tok, g_tok_unf, g_tok_rot, g_tok_step, caches
     torch.cuda.empty_cache()
     return out
 
@@ -1098,10 +1121,12 @@ def main() -> int:
                                        "algorithmic bytes and unmasked pairs",
                            **res["configs"]}
     if "workloads" in res:
-        line["workloads"] = {"workload": "BASELINE configs 3 and 4 through every layer: Gemma QK-norm + RoPE "
-                                         "prologue, then the fused prefill or decode step (attention + append); "
-                                         "5 local (sliding window) : 1 global layers; phases are the reference's "
-                                         "rotary / attention / kv_append buckets",
+        line["workloads"] = {"workload": "BASELINE configs 3 and 4 through every layer: prefill chunks = Gemma "
+                                         "QK-norm + RoPE prologue, then the fused prefill step (attention + "
+                                         "append); decode tokens = the Gemma decode step (QK-norm, RoPE, "
+                                         "attention, append in two launches; unfused_* = prologue launch + "
+                                         "decode step); 5 local (sliding window) : 1 global layers; phases are "
+                                         "the reference's rotary / attention / kv_append buckets",
                              **res["workloads"]}
     if cpu is not None:
         line["cpu_baseline"] = cpu

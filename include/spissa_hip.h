@@ -221,6 +221,20 @@ int spissa_decode_step_device(spissa_session *s, const spissa_rope_table *table,
                               const float *d_q, const float *d_k, const float *d_v,
                               spissa_kv_cache *const *caches, size_t batch,
                               const spissa_kv_attention_config *cfg, float *d_out);
+/* The Gemma 3 decode step of one layer in the same two launches: the
+ * QK-norm of q and the new key with the [head_dim] weights d_q_norm and
+ * d_k_norm (ops.rs:159-179), the Gemma RoPE from `table` (a GEMMA table over
+ * the whole head), q *= q_prescale, then the attention and the append, as
+ * models/gemma/generate.rs:232-295 runs them per layer (the prologue of
+ * spissa_gemma_qk_prologue_device followed by spissa_decode_step_device).
+ * d_q, d_k, d_v are read-only. The appended key is bit-identical to that
+ * sequence's; q's sum of squares is taken as a tree (it only enters the
+ * scores), so the output agrees within the attention's tolerance. */
+int spissa_gemma_decode_step_device(spissa_session *s, const spissa_rope_table *table,
+                                    const float *d_q, const float *d_k, const float *d_v,
+                                    spissa_kv_cache *const *caches, size_t batch,
+                                    const spissa_kv_attention_config *cfg, const float *d_q_norm,
+                                    const float *d_k_norm, float eps, float q_prescale, float *d_out);
 /* spissa_decode_step_device without any allocation. No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops). The split partials live in a
@@ -256,6 +270,7 @@ typedef struct {
     int tile_keys;          /* prefill: keys per tile */
     int workgroup_queries;  /* prefill: queries per workgroup */
     int o_split;            /* prefill: head_dim-256 output split over two waves */
+    int xcd_group;          /* prefill with key splits: the workgroups of one KV head's split share an XCD */
     long max_tiles;         /* prefill: most key tiles one unsplit workgroup visits */
     size_t workgroups;      /* attention kernel grid (decode: its first launch of <= 16 sequences) */
     size_t partial_bytes;   /* decode: split partials of the largest launch; prefill: key-split partials */

@@ -89,7 +89,7 @@ class AttentionPlanC(C.Structure):
         ("path", C.c_int), ("heads_per_block", C.c_int), ("head_blocks", C.c_int),
         ("keys_per_split", C.c_int), ("splits", C.c_int), ("tiles_per_split", C.c_int),
         ("tile_keys", C.c_int), ("workgroup_queries", C.c_int), ("o_split", C.c_int),
-        ("max_tiles", C.c_long), ("workgroups", c_size), ("partial_bytes", c_size), ("stage_bytes", c_size),
+        ("xcd_group", C.c_int), ("max_tiles", C.c_long), ("workgroups", c_size), ("partial_bytes", c_size), ("stage_bytes", c_size),
     ]
 
 
@@ -163,6 +163,10 @@ SIGNATURES = {
         C.c_int,
         [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, C.POINTER(c_void_p), c_size,
          C.POINTER(AttnConfigC), c_void_p]),
+    "spissa_gemma_decode_step_device": (
+        C.c_int,
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, C.POINTER(c_void_p), c_size,
+         C.POINTER(AttnConfigC), c_void_p, c_void_p, C.c_float, C.c_float, c_void_p]),
     "spissa_decode_step_device_noalloc": (
         C.c_int,
         [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, C.POINTER(c_void_p), c_size,

@@ -978,9 +978,10 @@ static bool plan_decode(int D, int Hq, int Hkv, size_t window, const int *past, 
     split_cap = (int)std::min<size_t>(fit, kMaxDecodeSplits);
   }
   p->kps = decode_keys_per_split(D, p->RB, total_rows, std::max(1, max_keys), split_cap);
-  p->max_splits = (max_keys + p->kps - 1) / p->kps;
+  // the last split of a sequence also takes its new token: at least one split
+  p->max_splits = std::max(1, (max_keys + p->kps - 1) / p->kps);
   p->workgroups = groups * p->max_splits;
-  p->partial_bytes = groups * std::max(1, p->max_splits) * entry;
+  p->partial_bytes = groups * p->max_splits * entry;
   return true;
 }
 
@@ -990,10 +991,15 @@ static bool plan_decode(int D, int Hq, int Hkv, size_t window, const int *past, 
 // capacity when `append` is set. The partials go to the session workspace,
 // or, with `fixed` set, to the fixed_bytes at `fixed` (splits are coarsened
 // to fit; the caller has checked that one split per group fits).
+struct GemmaQkNorm {  // fused QK-norm of the Gemma decode step
+  const float *q_norm, *k_norm;
+  float eps, q_prescale;
+};
+
 static int run_decode(spissa_session *s, const float *d_q, const float *d_k, const float *d_v,
                       const spissa_kv_cache *const *caches, size_t batch, const spissa_kv_attention_config *c,
                       float *d_out, const spissa_rope_table *table, bool append, float *fixed = nullptr,
-                      size_t fixed_bytes = 0) {
+                      size_t fixed_bytes = 0, const GemmaQkNorm *norm = nullptr) {
   const int D = (int)c->head_dim, Hq = (int)c->num_heads, Hkv = (int)c->kv_heads;
   const int R = Hq / Hkv;
   for (size_t b0 = 0; b0 < batch; b0 += kMaxDecodeBatch) {
@@ -1031,6 +1037,12 @@ static int run_decode(spissa_session *s, const float *d_q, const float *d_k, con
     a.rope_cos = table ? table->cos : nullptr;
     a.rope_sin = table ? table->sin : nullptr;
     a.do_append = append ? 1 : 0;
+    if (norm) {
+      a.q_norm = norm->q_norm;
+      a.k_norm = norm->k_norm;
+      a.norm_eps = norm->eps;
+      a.q_prescale = norm->q_prescale;
+    }
     a.B = B;
     a.Hq = Hq;
     a.Hkv = Hkv;
@@ -1112,7 +1124,10 @@ static void plan_prefill(PrefillArgs &a, int D, int cus, PrefillPlan *p) {
   // 10% faster on a 4096-token causal prefill at head_dim 256, 5-9% slower on
   // windowed and split ranges of 10-19 tiles).
   a.o_split = D >= 256 && (a.splits > 1 ? a.tps : p->tiles) >= 32;
-  p->workgroups = (size_t)base * a.splits;
+  a.xcd_group = prefill_use_xcd_group(a, D) ? 1 : 0;
+  const int wgq = prefill_wg_queries(a, D);
+  p->workgroups = (size_t)prefill_grid_workgroups((S + wgq - 1) / wgq, a.R / (128 / wgq), a.Hkv, a.splits,
+                                                  a.xcd_group);
 }
 
 static void prefill_args_base(PrefillArgs &a, const spissa_kv_attention_config *c, int P) {
@@ -1257,6 +1272,25 @@ extern "C" int spissa_decode_step_device(spissa_session *s, const spissa_rope_ta
   if (batch == 0) return SPISSA_OK;
   HIP_TRY(hipSetDevice(s->device));
   ST_TRY(run_decode(s, d_q, d_k, d_v, caches, batch, cfg, d_out, table, true));
+  for (size_t b = 0; b < batch; ++b) caches[b]->len += 1;
+  return SPISSA_OK;
+  GUARD_END
+}
+
+extern "C" int spissa_gemma_decode_step_device(spissa_session *s, const spissa_rope_table *table,
+                                               const float *d_q, const float *d_k, const float *d_v,
+                                               spissa_kv_cache *const *caches, size_t batch,
+                                               const spissa_kv_attention_config *cfg, const float *d_q_norm,
+                                               const float *d_k_norm, float eps, float q_prescale, float *d_out) {
+  GUARD_BEGIN
+  if (!table || !d_q_norm || !d_k_norm) return set_err(SPISSA_ERR_ARGUMENT, "null argument");
+  if (table->kind != SPISSA_ROPE_GEMMA)
+    return set_err(SPISSA_ERR_ARGUMENT, "the gemma decode step needs a gemma rope table");
+  ST_TRY(validate_decode_step(s, table, caches, batch, cfg));
+  if (batch == 0) return SPISSA_OK;
+  HIP_TRY(hipSetDevice(s->device));
+  const GemmaQkNorm norm{d_q_norm, d_k_norm, eps, q_prescale};
+  ST_TRY(run_decode(s, d_q, d_k, d_v, caches, batch, cfg, d_out, table, true, nullptr, 0, &norm));
   for (size_t b = 0; b < batch; ++b) caches[b]->len += 1;
   return SPISSA_OK;
   GUARD_END
@@ -1450,6 +1484,7 @@ extern "C" int spissa_plan_attention(const spissa_kv_attention_config *cfg, cons
     out->tile_keys = prefill_tile_keys(D);
     out->workgroup_queries = prefill_wg_queries(a, D);
     out->o_split = a.o_split;
+    out->xcd_group = a.xcd_group;
     out->max_tiles = p.tiles;
     out->workgroups = p.workgroups;
     out->partial_bytes = p.ppart_bytes;

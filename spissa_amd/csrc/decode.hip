@@ -3,7 +3,7 @@
 //
 // Two kernels per launch:
 //
-// 1. decode_split_kernel covers the cached keys only. One workgroup
+// 1. decode_split_kernel covers the keys. One workgroup
 //    (256 threads, 4 waves) owns a range of cached keys ("split") of one KV
 //    head for one sequence and serves RB query heads of that head's group, so
 //    every K/V row is read from HBM once per head block. A key row (D floats)
@@ -16,15 +16,16 @@
 //    v_permlane16/32_swap exchanges; each row group runs an online softmax in
 //    the log2 domain; the groups of a wave merge in registers (DPP row_ror:8,
 //    permlane swaps), the four waves through one LDS exchange, and every
-//    workgroup stores its partial (max, sum, unnormalised output).
+//    workgroup stores its partial (max, sum, unnormalised output). Split 0
+//    of a sequence (dispatched first) also takes the new token: its key
+//    (QK-normed and rotated in registers when those are fused) and value
+//    join as one more row, and with the fused append that workgroup writes
+//    them to cache row P, which no split reads.
 //
-// 2. decode_combine_kernel handles the new token itself (its optional RoPE,
-//    its score and value), merges it with the splits' partials into the
-//    normalised output, and optionally appends the new (rotated) key and
-//    value to the cache row it occupies. The kernel boundary publishes the
-//    partials across XCDs, so no in-kernel device-scope synchronisation is
-//    needed, and a whole decode step of a layer (RoPE, attention, append) is
-//    these two launches.
+// 2. decode_combine_kernel merges the splits' partials into the normalised
+//    output. The kernel boundary publishes the partials across XCDs, so no
+//    in-kernel device-scope synchronisation is needed, and a whole decode
+//    step of a layer (RoPE, attention, append) is these two launches.
 //
 // Errors. A zero or non-finite softmax denominator (rotary.rs:560-564) sets a
 // device error bit instead of aborting.
@@ -118,6 +119,9 @@ __device__ __forceinline__ float dot8(const float4 a0, const float4 a1, const fl
 __device__ __forceinline__ float4 scale4(float4 v, float s) {
   return make_float4(v.x * s, v.y * s, v.z * s, v.w * s);
 }
+__device__ __forceinline__ float4 mul4(float4 a, float4 b) {
+  return make_float4(a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w);
+}
 __device__ __forceinline__ float4 fma4(float p, float4 v, float4 acc) {
   return make_float4(fmaf(p, v.x, acc.x), fmaf(p, v.y, acc.y), fmaf(p, v.z, acc.z),
                      fmaf(p, v.w, acc.w));
@@ -137,6 +141,15 @@ __device__ __forceinline__ void rotate_pair(float &first, float &second, float c
   second = b;
 }
 
+// The rotation of a lane's two float4 (dims [4s, 4s+4) and [D/2 + 4s, ...),
+// rotate-half partners) by the table's cos/sin of those pairs.
+__device__ __forceinline__ void rotate4(float4 &x0, float4 &x1, const float4 c, const float4 s) {
+  rotate_pair(x0.x, x1.x, c.x, s.x);
+  rotate_pair(x0.y, x1.y, c.y, s.y);
+  rotate_pair(x0.z, x1.z, c.z, s.z);
+  rotate_pair(x0.w, x1.w, c.w, s.w);
+}
+
 }  // namespace
 
 // At least 4 waves per SIMD (<= 128 VGPRs): four workgroups per CU stay resident.
@@ -151,6 +164,7 @@ __global__ __launch_bounds__(256, 4) void decode_split_kernel(const DecodeArgs a
   __shared__ float red_o[NG][RB][D];
   __shared__ float red_l[NG][RB];
   __shared__ float wave_m[4][RB];
+  __shared__ float knorm_sq[D];  // squares of the new key (fused QK-norm)
 
   // Head blocks are the fastest grid dimension: the workgroups that read the
   // same key rows (all KV heads of one split) are dispatched back to back.
@@ -160,7 +174,9 @@ __global__ __launch_bounds__(256, 4) void decode_split_kernel(const DecodeArgs a
   const int b = blockIdx.z;
   const int P = a.seq[b].past;
   const int kstart = a.window > 0 ? max(0, P + 1 - a.window) : 0;
-  const int nsplit = (P - kstart + a.kps - 1) / a.kps;  // cached keys only
+  // The cached keys in splits of kps; split 0 also takes the new token (one
+  // split with no cached key when there are none).
+  const int nsplit = max(1, (P - kstart + a.kps - 1) / a.kps);
   if (split >= nsplit) return;
   const int k0 = kstart + split * a.kps;
   const int k1 = min(P, k0 + a.kps);
@@ -210,15 +226,30 @@ __global__ __launch_bounds__(256, 4) void decode_split_kernel(const DecodeArgs a
       qv[r][0] = ld4(qb + r * D + 4 * sub);
       qv[r][1] = ld4(qb + r * D + HALF + 4 * sub);
     }
+    if (a.q_norm) {
+      // Gemma QK-norm of q. The sum of squares is a tree over the row's lanes
+      // (q only enters the scores, which are compared within tolerance; the
+      // appended key below keeps the reference's sequential sum).
+      const float4 w0 = ld4(a.q_norm + 4 * sub), w1 = ld4(a.q_norm + HALF + 4 * sub);
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        const float ss = group_sum<LPR>(dot8(qv[r][0], qv[r][1], qv[r][0], qv[r][1]));
+        const float inv = 1.0f / sqrtf(ss / (float)D + a.norm_eps);
+        qv[r][0] = mul4(scale4(qv[r][0], inv), w0);
+        qv[r][1] = mul4(scale4(qv[r][1], inv), w1);
+      }
+    }
     if (a.rope_cos) {
       const float4 c = ld4(a.rope_cos + (long)P * HALF + 4 * sub);
       const float4 sn = ld4(a.rope_sin + (long)P * HALF + 4 * sub);
 #pragma unroll
+      for (int r = 0; r < RB; ++r) rotate4(qv[r][0], qv[r][1], c, sn);
+    }
+    if (a.q_norm) {
+#pragma unroll
       for (int r = 0; r < RB; ++r) {
-        rotate_pair(qv[r][0].x, qv[r][1].x, c.x, sn.x);
-        rotate_pair(qv[r][0].y, qv[r][1].y, c.y, sn.y);
-        rotate_pair(qv[r][0].z, qv[r][1].z, c.z, sn.z);
-        rotate_pair(qv[r][0].w, qv[r][1].w, c.w, sn.w);
+        qv[r][0] = scale4(qv[r][0], a.q_prescale);
+        qv[r][1] = scale4(qv[r][1], a.q_prescale);
       }
     }
   }
@@ -265,6 +296,72 @@ __global__ __launch_bounds__(256, 4) void decode_split_kernel(const DecodeArgs a
     }
   }
 
+  // ---- the new token (key P), in split 0: wave 0 adds it as one more row.
+  // Every row group of the wave loads the same row, so its scores are
+  // uniform and only group 0 adds the value. ----
+  if (split == 0 && wave == 0) {
+    const long row = ((long)b * a.Hkv + h) * D;
+    float4 kn0 = ld4(a.cur_k + row + 4 * sub), kn1 = ld4(a.cur_k + row + HALF + 4 * sub);
+    const float4 vn0 = ld4(a.cur_v + row + 4 * sub), vn1 = ld4(a.cur_v + row + HALF + 4 * sub);
+    const bool first = lane < LPR;
+    if (a.k_norm) {
+      // ops.rs:159-179 on the key row, bit for bit: the squares in index
+      // order through LDS, summed sequentially by lane 0, then x * inv * w.
+      if (first) {
+        *reinterpret_cast<float4 *>(&knorm_sq[4 * sub]) = mul4(kn0, kn0);
+        *reinterpret_cast<float4 *>(&knorm_sq[HALF + 4 * sub]) = mul4(kn1, kn1);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      float inv = 0.0f;
+      if (lane == 0) {
+        float acc = 0.0f;
+        for (int c = 0; c < D; ++c) acc += knorm_sq[c];
+        inv = 1.0f / sqrtf(acc / (float)D + a.norm_eps);
+      }
+      inv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv), 0));
+      kn0 = mul4(scale4(kn0, inv), ld4(a.k_norm + 4 * sub));
+      kn1 = mul4(scale4(kn1, inv), ld4(a.k_norm + HALF + 4 * sub));
+    }
+    if (a.rope_cos)
+      rotate4(kn0, kn1, ld4(a.rope_cos + (long)P * HALF + 4 * sub), ld4(a.rope_sin + (long)P * HALF + 4 * sub));
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const float dn = group_sum<LPR>(dot8(qv[r][0], qv[r][1], kn0, kn1)) * qs;
+      const float mnew = fmaxf(m[r], dn);
+      const float ms = safe_max(mnew);
+      const float alpha = fast_exp2(m[r] - ms);
+      const float p = first ? fast_exp2(dn - ms) : 0.0f;
+      l[r] = fmaf(l[r], alpha, p);
+      o[r][0] = fma4(p, vn0, scale4(o[r][0], alpha));
+      o[r][1] = fma4(p, vn1, scale4(o[r][1], alpha));
+      m[r] = mnew;
+    }
+    // append the rotated key and the value at cache row P (f32 rows, and the
+    // bf16 prefill operands when the cache has them)
+    if (a.do_append && hb == 0 && first) {
+      float *kd = a.app_k[b] + (long)h * D, *vd = a.app_v[b] + (long)h * D;
+      *reinterpret_cast<float4 *>(kd + 4 * sub) = kn0;
+      *reinterpret_cast<float4 *>(kd + HALF + 4 * sub) = kn1;
+      *reinterpret_cast<float4 *>(vd + 4 * sub) = vn0;
+      *reinterpret_cast<float4 *>(vd + HALF + 4 * sub) = vn1;
+      if (a.app_kb[b]) {
+        const long cap = a.app_cap[b];
+        bf16 *kb = a.app_kb[b] + ((long)h * cap + P) * D;
+        bf16 *vt = a.app_vt[b] + (long)h * D * cap + vt_key_slot(P);
+        const float kk[8] = {kn0.x, kn0.y, kn0.z, kn0.w, kn1.x, kn1.y, kn1.z, kn1.w};
+        const float vv[8] = {vn0.x, vn0.y, vn0.z, vn0.w, vn1.x, vn1.y, vn1.z, vn1.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int dim = (i < 4 ? 0 : HALF) + 4 * sub + (i & 3);
+          kb[dim] = (bf16)kk[i];
+          vt[(long)dim * cap] = (bf16)vv[i];
+        }
+      }
+    }
+  }
+
   // ---- merge: the groups of a wave share m, the four waves are rescaled ----
 #pragma unroll
   for (int r = 0; r < RB; ++r) {
@@ -302,9 +399,8 @@ __global__ __launch_bounds__(256, 4) void decode_split_kernel(const DecodeArgs a
   }
 }
 
-// Finishes the attention of one (sequence, KV head, head block): the new
-// token's score and value, merged with the partials of every split of the
-// cached keys, then the optional append of the new key and value.
+// Finishes the attention of one (sequence, KV head, head block): merges the
+// partials of every split (the last one holds the new token) into O / L.
 // Grid: (Hkv*HB, RB*D / OUTS, B), the head blocks fastest as in the split
 // kernel: consecutive workgroups go to consecutive XCDs, so the combine of a
 // head runs on the XCD whose workgroups wrote that head's partials (measured
@@ -314,29 +410,23 @@ __global__ __launch_bounds__(256, 4) void decode_split_kernel(const DecodeArgs a
 // splits in flight; the SL lanes of every output are merged through LDS.
 template <int D, int RB, int SL>
 __global__ __launch_bounds__(1024) void decode_combine_kernel(const DecodeArgs a) {
-  constexpr int HALF = D / 2;
   constexpr int ENTRY = RB * (D + 2);
   constexpr int OUTS = 1024 / SL, UNROLL = 8;  // one load round up to SL * 8 splits
   __shared__ float s_m[SL][OUTS], s_l[SL][OUTS], s_o[SL][OUTS];
-  __shared__ float s_dot[RB * D / 64];
-  __shared__ float s_new[RB];
 
   const int hb = blockIdx.x % a.HB;
   const int h = blockIdx.x / a.HB;
   const int b = blockIdx.z;
   const int P = a.seq[b].past;
   const int kstart = a.window > 0 ? max(0, P + 1 - a.window) : 0;
-  const int nsplit = (P - kstart + a.kps - 1) / a.kps;
+  const int nsplit = max(1, (P - kstart + a.kps - 1) / a.kps);
   const int tid = threadIdx.x;
   const int out = tid & (OUTS - 1);
   const int sl = tid / OUTS;
   const int e = blockIdx.y * OUTS + out;  // < RB*D: RB*D is a multiple of OUTS
   const int r = e / D;
   const int qh0 = h * a.R + hb * RB;
-  const float *knew = a.cur_k + ((long)b * a.Hkv + h) * D;
-  const float *vnew = a.cur_v + ((long)b * a.Hkv + h) * D;
 
-  // ---- loads first: the first batch of split partials, then the new token ----
   const long bhh = ((long)b * a.Hkv + h) * a.HB + hb;
   const float *ents = a.partial + bhh * a.max_splits * (long)ENTRY;
   float ms[UNROLL], ls[UNROLL], os[UNROLL];
@@ -356,32 +446,10 @@ __global__ __launch_bounds__(1024) void decode_combine_kernel(const DecodeArgs a
       }
     }
   };
-  load_batch(sl);
 
-  float kd = 0.0f;  // this thread's (rotated) key element, kept for the append
-  float prod = 0.0f;
-  if (tid < RB * D) {
-    const int rr = tid / D, d = tid % D;
-    const float *qrow = a.q + ((long)b * a.Hq + qh0 + rr) * D;
-    float qd = qrow[d];
-    kd = knew[d];
-    if (a.rope_cos) {
-      const int pair = d % HALF;
-      const float c = a.rope_cos[(long)P * HALF + pair], sn = a.rope_sin[(long)P * HALF + pair];
-      float q1 = qrow[pair], q2 = qrow[pair + HALF], k1 = knew[pair], k2 = knew[pair + HALF];
-      rotate_pair(q1, q2, c, sn);
-      rotate_pair(k1, k2, c, sn);
-      qd = d < HALF ? q1 : q2;
-      kd = d < HALF ? k1 : k2;
-    }
-    prod = qd * kd;
-  }
-  const float vd_out = vnew[e % D];
-
-  // ---- merge the splits ----
   float m = NEG_INF, l = 0.0f, o = 0.0f;
   for (int s0 = sl; s0 < nsplit; s0 += SL * UNROLL) {
-    if (s0 != sl) load_batch(s0);
+    load_batch(s0);
     float mx = m;
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) mx = fmaxf(mx, ms[u]);
@@ -397,31 +465,16 @@ __global__ __launch_bounds__(1024) void decode_combine_kernel(const DecodeArgs a
     }
     m = mx;
   }
-
-  // ---- the new token's score: q . k over the head, per query head ----
-  if (tid < RB * D) {
-    prod = group_sum<64>(prod);
-    if ((tid & 63) == 0) s_dot[tid >> 6] = prod;
-  }
   s_m[sl][out] = m;
   s_l[sl][out] = l;
   s_o[sl][out] = o;
   __syncthreads();
-  if (tid < RB) {
-    float dot = 0.0f;
-#pragma unroll
-    for (int w = 0; w < D / 64; ++w) dot += s_dot[tid * (D / 64) + w];
-    s_new[tid] = dot * a.qscale;
-  }
-  __syncthreads();
   if (sl == 0) {
-    const float sn = s_new[r];
-    float M = sn;
+    float M = NEG_INF;
 #pragma unroll
     for (int k = 0; k < SL; ++k) M = fmaxf(M, s_m[k][out]);
     const float Ms = safe_max(M);
-    const float pn = fast_exp2(sn - Ms);
-    float L = pn, O = pn * vd_out;
+    float L = 0.0f, O = 0.0f;
 #pragma unroll
     for (int k = 0; k < SL; ++k) {
       const float g = fast_exp2(s_m[k][out] - Ms);
@@ -430,17 +483,6 @@ __global__ __launch_bounds__(1024) void decode_combine_kernel(const DecodeArgs a
     }
     a.out[((long)b * a.Hq + qh0) * D + e] = O / L;
     if ((e % D) == 0 && !(L > 0.0f && L < __builtin_inff())) atomicOr(a.err, kDevErrSoftmaxDenominator);
-  }
-  // ---- append the new (rotated) key and value at cache row P ----
-  if (a.do_append && blockIdx.y == 0 && hb == 0 && tid < D) {
-    const float vd = vnew[tid];
-    a.app_k[b][(long)h * D + tid] = kd;
-    a.app_v[b][(long)h * D + tid] = vd;
-    if (a.app_kb[b]) {
-      const long cap = a.app_cap[b];
-      a.app_kb[b][((long)h * cap + P) * D + tid] = (bf16)kd;
-      a.app_vt[b][((long)h * D + tid) * cap + vt_key_slot(P)] = (bf16)vd;
-    }
   }
 }
 
@@ -455,7 +497,8 @@ constexpr int kCombineWideSplits = 128;
 
 template <int D, int RB>
 hipError_t launch_one(hipStream_t st, const DecodeArgs &a) {
-  if (a.max_splits > 0) {
+  if (a.max_splits < 1) return hipErrorInvalidValue;  // the new token needs a split
+  {
     dim3 grid((unsigned)(a.Hkv * a.HB), (unsigned)a.max_splits, (unsigned)a.B);
     hipLaunchKernelGGL((decode_split_kernel<D, RB, rows_per_group(RB)>), grid, dim3(256), 0, st, a);
     hipError_t e = hipGetLastError();

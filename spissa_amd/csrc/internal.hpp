@@ -60,6 +60,12 @@ struct DecodeArgs {
   bf16 *app_vt[kMaxDecodeBatch];
   long app_cap[kMaxDecodeBatch];
   int do_append;
+  // Fused Gemma QK-norm (models/gemma/generate.rs:232-275), null: none. q and
+  // the new key are RMS-normed with these [D] weights before RoPE, and q is
+  // multiplied by q_prescale after it.
+  const float *q_norm;
+  const float *k_norm;
+  float norm_eps, q_prescale;
   int B, Hq, Hkv, R, HB;  // R = Hq/Hkv, HB = head blocks per kv head
   int window;
   int kps;             // cached keys per split
@@ -110,6 +116,11 @@ struct PrefillArgs {
   // 1.5x the MFMAs (both waves compute the scores) and doubles the waves per
   // SIMD, which pays off on long key ranges per workgroup.
   int o_split;
+  // With key splits: the workgroups that read one KV head's split (its head
+  // blocks and query blocks) are given ids 8 apart, so they run on one XCD
+  // and share its L2 (prefill_use_xcd_group decides; the grid is padded to a
+  // multiple of 8 units).
+  int xcd_group;
 };
 
 // Workgroup slots per CU and key-tile width of the prefill kernels, and the
@@ -121,6 +132,10 @@ int prefill_wg_queries(const PrefillArgs &a, int D);
 long prefill_base_workgroups(const PrefillArgs &a, int D);
 // Most key tiles one (unsplit) prefill workgroup visits.
 long prefill_max_tile_span(const PrefillArgs &a, int D);
+// Workgroups of a prefill launch of n_qblocks x head_blocks x Hkv x splits
+// (grouped by XCD: units of one KV head and split padded to a multiple of 8).
+long prefill_grid_workgroups(long n_qblocks, long head_blocks, long Hkv, long splits, int xcd_group);
+bool prefill_use_xcd_group(const PrefillArgs &a, int D);
 
 struct GenericArgs {
   const float *q;  // [S, Hq, D]

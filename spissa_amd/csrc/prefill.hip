@@ -191,13 +191,30 @@ prefill_kernel(const PrefillArgs a) {
   __shared__ __attribute__((aligned(1024))) char v_lds1[G::VBYTES];
 
   const int HB = a.R / RB;
-  int bid = blockIdx.x;
-  const int hh = bid % (a.Hkv * HB);
-  bid /= (a.Hkv * HB);
-  const int split = bid % a.splits;
-  bid /= a.splits;
-  const int qt = a.n_qblocks - 1 - bid;  // longest rows first
-  const int h = hh / HB, hb = hh % HB;
+  int h, hb, split, qt;
+  if (a.xcd_group) {
+    // Workgroup ids 8 apart run on one XCD. The HB * n_qblocks workgroups
+    // that read the same keys (one KV head, one split) get ids
+    // lo + 8 * (g + G * hi), unit = 8 * hi + lo, so that they share that
+    // XCD's L2 instead of each fetching the keys from HBM.
+    const int G = HB * a.n_qblocks;
+    const int lo = (int)(blockIdx.x & 7), rest = (int)(blockIdx.x >> 3);
+    const int g = rest % G, unit = (rest / G) * 8 + lo;
+    if (unit >= a.Hkv * a.splits) return;  // padding up to a multiple of 8 units
+    h = unit % a.Hkv;
+    split = unit / a.Hkv;
+    hb = g % HB;
+    qt = a.n_qblocks - 1 - g / HB;
+  } else {
+    int bid = blockIdx.x;
+    const int hh = bid % (a.Hkv * HB);
+    bid /= (a.Hkv * HB);
+    split = bid % a.splits;
+    bid /= a.splits;
+    qt = a.n_qblocks - 1 - bid;  // longest rows first
+    h = hh / HB;
+    hb = hh % HB;
+  }
   // The wave index is uniform: readfirstlane keeps it (and all that derives
   // from it) in scalar registers and wave-level branches uniform.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -606,7 +623,7 @@ template <int D, int RB, int NPB, int BN, int QB, int OS>
 hipError_t launch_shape(hipStream_t st, PrefillArgs a) {
   constexpr int WGQ = NPB * QB * 32;
   a.n_qblocks = (a.S + WGQ - 1) / WGQ;
-  const long blocks = (long)a.n_qblocks * a.splits * a.Hkv * (a.R / RB);
+  const long blocks = prefill_grid_workgroups(a.n_qblocks, a.R / RB, a.Hkv, a.splits, a.xcd_group);
   hipLaunchKernelGGL((prefill_kernel<D, RB, NPB, BN, QB, OS>), dim3((unsigned)blocks), dim3(RB * NPB * OS * 64), 0,
                      st, a);
   return hipGetLastError();
@@ -652,6 +669,18 @@ long prefill_base_workgroups(const PrefillArgs &a, int D) {
   const int wgq = prefill_wg_queries(a, D);
   const int rb = 128 / wgq;
   return (long)((a.S + wgq - 1) / wgq) * a.Hkv * (a.R / rb);
+}
+
+long prefill_grid_workgroups(long n_qblocks, long head_blocks, long Hkv, long splits, int xcd_group) {
+  if (!xcd_group) return n_qblocks * head_blocks * Hkv * splits;
+  const long units = (Hkv * splits + 7) / 8 * 8;
+  return units * head_blocks * n_qblocks;
+}
+
+bool prefill_use_xcd_group(const PrefillArgs &a, int D) {
+  const int wgq = prefill_wg_queries(a, D);
+  const long G = (long)(a.R / (128 / wgq)) * ((a.S + wgq - 1) / wgq);
+  return a.splits > 1 && (long)a.Hkv * a.splits >= 8 && G > 1;
 }
 
 // The largest t_end - t_begin of prefill_kernel over its query blocks, with

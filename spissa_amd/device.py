@@ -226,6 +226,19 @@ class Session:
             self.handle, None if table is None else table.handle, _dev(q, "q"), _dev(k, "k"),
             _dev(v, "v"), arr, len(caches), C.byref(cfg), _dev(out, "out")))
 
+    def gemma_decode_step(self, table: RopeTable, q, k, v, caches: Sequence[KvCache], config: KvAttentionConfig,
+                          q_norm, k_norm, eps: float, q_prescale: float, out) -> None:
+        """The Gemma 3 decode step (spissa_gemma_decode_step_device): QK-norm with the
+        [D] weights q_norm / k_norm, Gemma RoPE from `table`, q *= q_prescale, then
+        attention and append, in the decode step's two launches; q/k/v read-only."""
+        arr = (_ffi.c_void_p * max(1, len(caches)))()
+        for i, c in enumerate(caches):
+            arr[i] = c.handle.value
+        cfg = config._c()
+        check(self._lib.spissa_gemma_decode_step_device(
+            self.handle, table.handle, _dev(q, "q"), _dev(k, "k"), _dev(v, "v"), arr, len(caches), C.byref(cfg),
+            _dev(q_norm, "q_norm"), _dev(k_norm, "k_norm"), float(eps), float(q_prescale), _dev(out, "out")))
+
     def decode_step_noalloc(self, table: Optional[RopeTable], q, k, v, caches: Sequence[KvCache],
                             config: KvAttentionConfig, out) -> None:
         """decode_step through spissa_decode_step_device_noalloc: no device allocation; the

@@ -30,7 +30,8 @@ TILE_ALIGN = 64
 def check_decode(cfg, past, plan, noalloc=False):
     """decode_split_kernel: grid (Hkv*HB, max_splits, B); split s of sequence b
     covers cached keys [kstart + s*kps, min(P, kstart + (s+1)*kps)) where
-    kstart = max(0, P + 1 - W) with a window; the new token is the combine's."""
+    kstart = max(0, P + 1 - W) with a window; the first of its
+    max(1, ceil((P - kstart) / kps)) splits also takes the new token (key P)."""
     D, Hq, Hkv, W = cfg.head_dim, cfg.num_heads, cfg.kv_heads, cfg.window
     assert plan["path"] == _ffi.KERNEL_DECODE
     RB, HB, kps = plan["heads_per_block"], plan["head_blocks"], plan["keys_per_split"]
@@ -39,33 +40,70 @@ def check_decode(cfg, past, plan, noalloc=False):
     B = min(len(past), MAX_DECODE_BATCH)  # the plan describes the first launch
     max_splits = plan["splits"]
     assert max_splits <= MAX_DECODE_SPLITS
+    assert max_splits >= 1
     assert plan["workgroups"] == B * Hkv * HB * max_splits
     groups = B * Hkv * HB
-    assert plan["partial_bytes"] >= groups * max(1, max_splits) * entry * 4
+    assert plan["partial_bytes"] >= groups * max_splits * entry * 4
     if noalloc:
         assert plan["partial_bytes"] <= SCRATCH_BYTES
     for b in range(B):
         P = past[b]
         kstart = max(0, P + 1 - W) if W > 0 else 0
-        nsplit = -(-(P - kstart) // kps)
+        nsplit = max(1, -(-(P - kstart) // kps))
         assert nsplit <= max_splits
         covered = []
         for s in range(nsplit):
             k0 = kstart + s * kps
             k1 = min(P, k0 + kps)
-            assert k0 < k1
+            assert k0 < k1 or (s == 0 and P == kstart)  # split 0 holds at least the new token
             covered.append((k0, k1))
             for h in range(Hkv):
                 for hb in range(HB):
                     bhh = (b * Hkv + h) * HB + hb
                     end = ((bhh * max_splits + s) + 1) * entry  # floats written by this split
                     assert end * 4 <= plan["partial_bytes"]
-        # contiguous, disjoint, exactly [kstart, P)
+        # contiguous, disjoint, exactly [kstart, P), and key P in split 0
         pos = kstart
         for k0, k1 in covered:
             assert k0 == pos
             pos = k1
         assert pos == P
+
+
+def check_prefill_grid(plan, n_qblocks, Hkv, HB, splits):
+    """prefill_kernel's workgroup id -> (KV head, head block, split, query
+    block) decode: every tuple exactly once; with xcd_group, the workgroups of
+    one (KV head, split) have ids equal mod 8 (one XCD) and the padding ids
+    decode to units past the last."""
+    G = HB * n_qblocks
+    units = Hkv * splits
+    seen, xcd = set(), {}
+    if plan["xcd_group"]:
+        assert splits > 1 and units >= 8 and G > 1
+        assert plan["workgroups"] == -(-units // 8) * 8 * G
+    else:
+        assert plan["workgroups"] == units * G
+    for bid in range(plan["workgroups"]):
+        if plan["xcd_group"]:
+            lo, rest = bid & 7, bid >> 3
+            g, unit = rest % G, (rest // G) * 8 + lo
+            if unit >= units:
+                continue
+            h, split, hb, qt = unit % Hkv, unit // Hkv, g % HB, n_qblocks - 1 - g // HB
+        else:
+            r = bid
+            hh = r % (Hkv * HB)
+            r //= Hkv * HB
+            split, qt = r % splits, n_qblocks - 1 - r // splits
+            h, hb = hh // HB, hh % HB
+        assert 0 <= qt < n_qblocks
+        key = (h, hb, split, qt)
+        assert key not in seen
+        seen.add(key)
+        xcd.setdefault((h, split), set()).add(bid % 8)
+    assert len(seen) == units * G
+    if plan["xcd_group"]:
+        assert all(len(v) == 1 for v in xcd.values())
 
 
 def check_prefill(cfg, P, plan):
@@ -81,7 +119,7 @@ def check_prefill(cfg, P, plan):
     key_total = P + S
     n_qblocks = -(-S // WGQ)
     rb = 128 // WGQ
-    assert plan["workgroups"] == n_qblocks * Hkv * (Hq // Hkv // rb) * splits
+    check_prefill_grid(plan, n_qblocks, Hkv, Hq // Hkv // rb, splits)
     P8 = P & ~(TILE_ALIGN - 1)
     cap_stage = ((P + S + TILE_ALIGN - 1) & ~(TILE_ALIGN - 1)) - P8
     assert plan["stage_bytes"] == 2 * Hkv * cap_stage * D * 2
@@ -178,6 +216,17 @@ def test_noalloc_plan_rejects_partials_beyond_the_scratch_array():
 def test_prefill_plan_covers_every_key(name, S, P, Hq, Hkv, D, W, causal):
     cfg = KvAttentionConfig(S, Hq, Hkv, D, causal, W)
     check_prefill(cfg, P, plan_attention(cfg, [P]))
+
+
+def test_split_prefill_groups_shared_keys_on_one_xcd():
+    # Gemma-3-4B chunk: 4 KV heads x 31 splits, two 64-query workgroups per split
+    plan = plan_attention(KvAttentionConfig(128, 8, 4, 256, True, 0), [16384])
+    assert plan["splits"] > 1 and plan["xcd_group"] == 1
+    # Llama-3.2-3B chunk: three head blocks of one KV head read the same keys
+    plan = plan_attention(KvAttentionConfig(128, 24, 8, 128, True, 0), [8192])
+    assert plan["splits"] > 1 and plan["xcd_group"] == 1
+    # unsplit prefill keeps the longest-first order
+    assert plan_attention(KvAttentionConfig(4096, 24, 8, 128, True, 0), [0])["xcd_group"] == 0
 
 
 def test_prefill_plan_sweep():
