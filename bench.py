@@ -529,16 +529,16 @@ def workloads_bench(sess, stream, gen, dev, args, time_graph) -> dict:
     reference's per-layer order (models/gemma/generate.rs:232-295): the QK-norm
     + Gemma RoPE + prescale prologue of the layer's new q and k rows, the
     attention over the cache and the new rows, the append. Prefill chunks run
-    the prologue (spissa_gemma_qk_prologue_device) and then the fused prefill
-    step; a decode token runs spissa_gemma_decode_step_device, which does all
-    of it in two launches. Local layers use the sliding window with RoPE base
+    spissa_gemma_prefill_step_device (1/rms pass, append with the norm and
+    RoPE folded in, attention); a decode token runs
+    spissa_gemma_decode_step_device, which does all of it in two launches. Local layers use the sliding window with RoPE base
     1e4; global layers ((l + 1) % 6 == 0) see every key, RoPE base 1e6 with
     position divisor 8. Each workload is one graph per phase set; the phases
     are the reference's buckets (session.rs:14-32): rotary (the prologue),
     attention and kv_append (the fused step's append pass, where it is a
-    launch of its own). A decode token's buckets are timed on the unfused
-    sequence (prologue launch, then the decode step), which is also reported
-    whole beside the fused step."""
+    launch of its own). The buckets are timed on the unfused sequence
+    (prologue launch, then the prefill or decode step), which is also
+    reported whole beside the fused steps."""
     import torch
 
     from spissa_amd import _ffi
@@ -589,27 +589,41 @@ def workloads_bench(sess, stream, gen, dev, args, time_graph) -> dict:
 
     def layers():
         for l in range(L):
+            sess.gemma_prefill_step(tab[kinds[l]], q[l], k[l], v[l], caches[l], cfgs[l], qn[l], kn[l], 1e-6, 1.0,
+                                    o[l])
+
+    def unfused():
+        for l in range(L):
             sess.gemma_qk_prologue(tab[kinds[l]], q[l], k[l], S, hq, hkv, d, qn[l], kn[l], 1e-6, 0, 1.0)
             sess.prefill_step(None, q[l], k[l], v[l], caches[l], cfgs[l], o[l])
 
+    def reset():
+        for c in caches:
+            c.truncate(0)
+
     steps()
     sess.sync()
-    for c in caches:
-        c.truncate(0)
-    g_all, g_pro, g_step = captured(layers), captured(prologue), None
-    for c in caches:
-        c.truncate(0)
+    reset()
+    layers()
+    sess.sync()
+    reset()
+    g_all = captured(layers)
+    reset()
+    g_unf, g_pro = captured(unfused), captured(prologue)
+    reset()
     g_step = captured(steps)
     g_att = captured(attention)  # the caches hold the prompt after the step's capture
     reps = max(3, args.steps // 4)
-    ms = {n: time_graph(g, reps, 2) for n, g in (("all", g_all), ("rotary", g_pro), ("step", g_step),
-                                                  ("attention", g_att))}
+    ms = {n: time_graph(g, reps, 2) for n, g in (("all", g_all), ("unfused", g_unf), ("rotary", g_pro),
+                                                  ("step", g_step), ("attention", g_att))}
     rec = {"layers": L, "global_layers": [l for l in range(L) if kinds[l]],
            "prefill_4096": {"ms": round(ms["all"], 3), "tokens_per_s": round(S / (ms["all"] * 1e-3), 1),
                             "us_per_layer": round(ms["all"] * 1e3 / L, 2),
-                            "phases_ms": {"rotary": round(ms["rotary"], 3), "attention": round(ms["attention"], 3),
-                                          "kv_append": round(ms["step"] - ms["attention"], 3)}}}
-    del g_all, g_pro, g_step, g_att, q, k, v, o, caches
+                            "unfused_ms": round(ms["unfused"], 3),
+                            "unfused_phases_ms": {"rotary": round(ms["rotary"], 3),
+                                                  "attention": round(ms["attention"], 3),
+                                                  "kv_append": round(ms["step"] - ms["attention"], 3)}}}
+    del g_all, g_unf, g_pro, g_step, g_att, q, k, v, o, caches
     torch.cuda.empty_cache()
 
     P = 32768
@@ -696,9 +710,8 @@ def workloads_bench(sess, stream, gen, dev, args, time_graph) -> dict:
 
     def chunk():
         for l in range(L):
-            pos = caches[l].len()
-            sess.gemma_qk_prologue(tab[kinds[l]], cq[l], ck[l], S, hq, hkv, d, qn[l], kn[l], 1e-6, pos, 1.0)
-            sess.prefill_step(None, cq[l], ck[l], cv[l], caches[l], ccfg[l], co[l])
+            sess.gemma_prefill_step(tab[kinds[l]], cq[l], ck[l], cv[l], caches[l], ccfg[l], qn[l], kn[l], 1e-6, 1.0,
+                                    co[l])
 
     def decode_token():
         for l in range(L):
@@ -1121,12 +1134,11 @@ def main() -> int:
                                        "algorithmic bytes and unmasked pairs",
                            **res["configs"]}
     if "workloads" in res:
-        line["workloads"] = {"workload": "BASELINE configs 3 and 4 through every layer: prefill chunks = Gemma "
-                                         "QK-norm + RoPE prologue, then the fused prefill step (attention + "
-                                         "append); decode tokens = the Gemma decode step (QK-norm, RoPE, "
-                                         "attention, append in two launches; unfused_* = prologue launch + "
-                                         "decode step); 5 local (sliding window) : 1 global layers; phases are "
-                                         "the reference's rotary / attention / kv_append buckets",
+        line["workloads"] = {"workload": "BASELINE configs 3 and 4 through every layer: the Gemma prefill and "
+                                         "decode steps (QK-norm, RoPE, attention, append fused; unfused_* = the "
+                                         "prologue launch, then the prefill or decode step); 5 local (sliding "
+                                         "window) : 1 global layers; phases are the reference's rotary / "
+                                         "attention / kv_append buckets, timed on the unfused sequence",
                              **res["workloads"]}
     if cpu is not None:
         line["cpu_baseline"] = cpu

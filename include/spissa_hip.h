@@ -301,6 +301,18 @@ int spissa_plan_attention(const spissa_kv_attention_config *cfg, const size_t *p
 int spissa_prefill_step_device(spissa_session *s, const spissa_rope_table *table, const float *d_q,
                                const float *d_k, const float *d_v, spissa_kv_cache *cache,
                                const spissa_kv_attention_config *cfg, float *d_out);
+/* The Gemma 3 prefill (or chunk) step of one layer: the QK-norm of the
+ * chunk's q and k rows with the [head_dim] weights (ops.rs:159-179), the
+ * Gemma RoPE from `table` (a GEMMA table over the whole head), q *= q_prescale,
+ * attention and append, as models/gemma/generate.rs:232-295 runs them per
+ * layer (spissa_gemma_qk_prologue_device then spissa_prefill_step_device, to
+ * the bit: the norm, with the sum of squares in index order, is folded into
+ * the append pass). d_q, d_k, d_v are
+ * read-only. query_len == 1 runs spissa_gemma_decode_step_device. */
+int spissa_gemma_prefill_step_device(spissa_session *s, const spissa_rope_table *table, const float *d_q,
+                                     const float *d_k, const float *d_v, spissa_kv_cache *cache,
+                                     const spissa_kv_attention_config *cfg, const float *d_q_norm,
+                                     const float *d_k_norm, float eps, float q_prescale, float *d_out);
 
 /* The attention of rotary.rs:335-415 in append-first order: the chunk's keys
  * and values are already the cache's last cfg->query_len rows (appended

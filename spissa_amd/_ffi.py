@@ -176,6 +176,10 @@ SIGNATURES = {
         [C.POINTER(AttnConfigC), C.POINTER(c_size), c_size, C.c_int, C.c_int, C.c_int,
          C.POINTER(AttentionPlanC)]),
     "spissa_hbm_read_probe_device": (C.c_int, [c_void_p, c_void_p, c_size, c_void_p]),
+    "spissa_gemma_prefill_step_device": (
+        C.c_int,
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, C.POINTER(AttnConfigC), c_void_p, c_void_p,
+         C.c_float, C.c_float, c_void_p]),
     "spissa_prefill_step_device": (
         C.c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, C.POINTER(AttnConfigC), c_void_p]),
     "spissa_attention_cached_device": (

@@ -1355,12 +1355,11 @@ static int launch_prefill_from_shadow(spissa_session *s, PrefillArgs &a, const s
   return SPISSA_OK;
 }
 
-extern "C" int spissa_prefill_step_device(spissa_session *s, const spissa_rope_table *table, const float *d_q,
-                                          const float *d_k, const float *d_v, spissa_kv_cache *cache,
-                                          const spissa_kv_attention_config *cfg, float *d_out) {
-  GUARD_BEGIN
-  if (!s || !cfg || !cache) return set_err(SPISSA_ERR_ARGUMENT, "null argument");
-  if (cfg->query_len == 1) return spissa_decode_step_device(s, table, d_q, d_k, d_v, &cache, 1, cfg, d_out);
+// The fused prefill step (RoPE, append, attention over the shadow), with the
+// Gemma QK-norm folded into the append when `norm` is set.
+static int run_prefill_step(spissa_session *s, const spissa_rope_table *table, const float *d_q, const float *d_k,
+                            const float *d_v, spissa_kv_cache *cache, const spissa_kv_attention_config *cfg,
+                            float *d_out, const GemmaQkNorm *norm) {
   ST_TRY(validate_attention(0, 0, 0, cache, cfg, false));
   size_t n, nl;  // rotary.rs:227-251: the append must fit before anything runs
   ST_TRY(kv_validate_append(cache, 0, 0, cfg->query_len, false, &n, &nl));
@@ -1387,12 +1386,39 @@ extern "C" int spissa_prefill_step_device(spissa_session *s, const spissa_rope_t
   ST_TRY(ensure_buf(s, s->qstage, S * cfg->num_heads * cfg->head_dim * sizeof(bf16)));
   if (plan.ppart_bytes) ST_TRY(ensure_buf(s, s->ppart, plan.ppart_bytes));
   bf16 *qb = (bf16 *)s->qstage.p;
+  PrefillNorm pn{};
+  if (norm) pn = PrefillNorm{norm->q_norm, norm->k_norm, norm->eps, norm->q_prescale};
   HIP_TRY(launch_prefill_append(s->stream, d_q, d_k, d_v, table ? table->cos : nullptr, table ? table->sin : nullptr,
                                 P, S, cfg->kv_heads, cfg->num_heads, cfg->head_dim, cache->keys, cache->values,
-                                cache->kb, cache->vt, cache->shadow_cap, qb, a.qk_scale_log2));
+                                cache->kb, cache->vt, cache->shadow_cap, qb, a.qk_scale_log2, norm ? &pn : nullptr));
   ST_TRY(launch_prefill_from_shadow(s, a, cache, d_q, qb, d_out, D));
   cache->len = nl;
   return SPISSA_OK;
+}
+
+extern "C" int spissa_prefill_step_device(spissa_session *s, const spissa_rope_table *table, const float *d_q,
+                                          const float *d_k, const float *d_v, spissa_kv_cache *cache,
+                                          const spissa_kv_attention_config *cfg, float *d_out) {
+  GUARD_BEGIN
+  if (!s || !cfg || !cache) return set_err(SPISSA_ERR_ARGUMENT, "null argument");
+  if (cfg->query_len == 1) return spissa_decode_step_device(s, table, d_q, d_k, d_v, &cache, 1, cfg, d_out);
+  return run_prefill_step(s, table, d_q, d_k, d_v, cache, cfg, d_out, nullptr);
+  GUARD_END
+}
+
+extern "C" int spissa_gemma_prefill_step_device(spissa_session *s, const spissa_rope_table *table, const float *d_q,
+                                                const float *d_k, const float *d_v, spissa_kv_cache *cache,
+                                                const spissa_kv_attention_config *cfg, const float *d_q_norm,
+                                                const float *d_k_norm, float eps, float q_prescale, float *d_out) {
+  GUARD_BEGIN
+  if (!s || !cfg || !cache || !table || !d_q_norm || !d_k_norm) return set_err(SPISSA_ERR_ARGUMENT, "null argument");
+  if (table->kind != SPISSA_ROPE_GEMMA)
+    return set_err(SPISSA_ERR_ARGUMENT, "the gemma prefill step needs a gemma rope table");
+  if (cfg->query_len == 1)
+    return spissa_gemma_decode_step_device(s, table, d_q, d_k, d_v, &cache, 1, cfg, d_q_norm, d_k_norm, eps,
+                                           q_prescale, d_out);
+  const GemmaQkNorm norm{d_q_norm, d_k_norm, eps, q_prescale};
+  return run_prefill_step(s, table, d_q, d_k, d_v, cache, cfg, d_out, &norm);
   GUARD_END
 }
 

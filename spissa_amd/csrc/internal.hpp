@@ -165,10 +165,18 @@ hipError_t launch_gemma_prologue(hipStream_t st, const float *cos_tab, const flo
 // rotated with cos/sin rows at positions P + i) into cache rows [P, P + S)
 // and the bf16 shadow (zeros up to the next multiple of 64), and q rotated,
 // scaled by qscale and rounded into qb [S, Hq, D] bf16. D % 64 == 0.
+// Fused Gemma QK-norm of the prefill step's append (null q_norm: none): q
+// and k rows are RMS-normed with the [D] weights before RoPE (the sum of
+// squares in index order, ops.rs:159-179), and q is multiplied by q_prescale
+// after it (models/gemma/generate.rs:232-275).
+struct PrefillNorm {
+  const float *q_norm, *k_norm;  // [D]
+  float eps, q_prescale;
+};
 hipError_t launch_prefill_append(hipStream_t st, const float *q, const float *k, const float *v,
                                  const float *cos_tab, const float *sin_tab, size_t P, size_t S, size_t H,
                                  size_t Hq, size_t D, float *cache_k, float *cache_v, bf16 *kb, bf16 *vt,
-                                 size_t cap, bf16 *qb, float qscale);
+                                 size_t cap, bf16 *qb, float qscale, const PrefillNorm *norm = nullptr);
 // Writes rows [0, n) and zero rows [n, n_pad) at buffer positions dst_first + i.
 hipError_t launch_stage_bf16(hipStream_t st, const float *k_rows, const float *v_rows, size_t n,
                              size_t n_pad, size_t H, size_t D, bf16 *kb, bf16 *vt,

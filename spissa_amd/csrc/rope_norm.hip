@@ -320,16 +320,58 @@ __global__ __launch_bounds__(256) void stage_bf16_kernel(const float *__restrict
 //   Q blocks (blockIdx.y >= H): query row i, rotated at position P + i,
 //     times qscale, rounded to bf16 into qb [S, Hq, D] -- the prefill
 //     kernel's Q operand, the same bits it would form from the rotated f32 row.
+// 1 / sqrt(mean(x^2) + eps) of a row of D floats held by a quad of lanes
+// (lane c of the quad holds dims 32z + 8c + [0, 8) and D/2 + 32z + 8c + [0, 8)
+// for every z), with the sum of squares taken in index order as
+// ops.rs:159-179 takes it: the running sum visits the lanes in dim order,
+// eight rounded squares at a time, passed on with a quad rotation (DPP).
+template <int D>
+__device__ __forceinline__ float quad_inv_rms(const float *row, int c, float eps) {
+#pragma clang fp contract(off)
+  constexpr int HALF = D / 2, G = HALF / 32;
+  float4 x[2][G][2];
+#pragma unroll
+  for (int part = 0; part < 2; ++part)
+#pragma unroll
+    for (int z = 0; z < G; ++z) {
+      x[part][z][0] = *reinterpret_cast<const float4 *>(row + part * HALF + 32 * z + 8 * c);
+      x[part][z][1] = *reinterpret_cast<const float4 *>(row + part * HALF + 32 * z + 8 * c + 4);
+    }
+  float acc = 0.0f;
+#pragma unroll
+  for (int part = 0; part < 2; ++part)
+#pragma unroll
+    for (int z = 0; z < G; ++z) {
+      const float *v = reinterpret_cast<const float *>(x[part][z]);
+#pragma unroll
+      for (int turn = 0; turn < 4; ++turn) {
+        float t = acc;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t = t + v[j] * v[j];
+        acc = c == turn ? t : acc;
+        // lane c takes lane c - 1's sum (quad_perm [3, 0, 1, 2])
+        acc = __builtin_amdgcn_update_dpp(acc, acc, 0x93, 0xf, 0xf, false);
+      }
+    }
+  // lane 0 of the quad holds the total; every lane takes it (quad_perm [0, 0, 0, 0])
+  acc = __builtin_amdgcn_update_dpp(acc, acc, 0x00, 0xf, 0xf, false);
+  const float mean_square = acc / (float)D;
+  return 1.0f / sqrtf(mean_square + eps);
+}
+
 // A block owns 64 positions and the 32 rotary pairs [32z, 32z + 32) of one
 // head, i.e. dims [32z, +32) and [D/2 + 32z, +32); thread t holds position
 // t / 4 and the eight pairs 8(t % 4) .. +7 of that range: a float4 pair of
 // each half. Values pass through an LDS tile for the V^T stores.
-// Grid: (position blocks, H + Hq, D / 64), 256 threads.
+// Grid: (position blocks, H + Hq, D / 64), 256 threads. NORM_D: 0, or the
+// head dim with the Gemma QK-norm folded in (each quad of lanes first takes
+// its full row's 1/rms).
+template <int NORM_D>
 __global__ __launch_bounds__(256) void prefill_append_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
     const float *__restrict__ cos_tab, const float *__restrict__ sin_tab, long P, long S, int H, int Hq, int D,
     float *__restrict__ cache_k, float *__restrict__ cache_v, bf16 *__restrict__ kb, bf16 *__restrict__ vt,
-    long cap, long pad_end, bf16 *__restrict__ qb, float qscale) {
+    long cap, long pad_end, bf16 *__restrict__ qb, float qscale, const PrefillNorm nrm) {
 #pragma clang fp contract(off)
   typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
   __shared__ float tile[64][65];  // V[position][lo 32 | hi 32 dims], padded against bank conflicts
@@ -369,6 +411,23 @@ __global__ __launch_bounds__(256) void prefill_append_kernel(
     *reinterpret_cast<float4 *>(p) = x[0];
     *reinterpret_cast<float4 *>(p + 4) = x[1];
   };
+  auto row_inv = [&](const float *row) {
+    if constexpr (NORM_D > 0) return quad_inv_rms<NORM_D>(row, c, nrm.eps);
+    return 1.0f;
+  };
+  // Gemma QK-norm of a row's eight pairs: (x * inv) * w, as the prologue.
+  auto norm = [&](float4 (&lo)[2], float4 (&hi)[2], float inv, const float *w) {
+    float4 wl[2], wh[2];
+    load2(w + p0, wl);
+    load2(w + half + p0, wh);
+    float *a = reinterpret_cast<float *>(lo), *b = reinterpret_cast<float *>(hi);
+    const float *x = reinterpret_cast<const float *>(wl), *y = reinterpret_cast<const float *>(wh);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      a[j] = a[j] * inv * x[j];
+      b[j] = b[j] * inv * y[j];
+    }
+  };
 
   if (!kv) {
     const int hq = blockIdx.y - H;
@@ -378,7 +437,17 @@ __global__ __launch_bounds__(256) void prefill_append_kernel(
     float4 lo[2], hi[2];
     load2(src + p0, lo);
     load2(src + half + p0, hi);
+    if (NORM_D) norm(lo, hi, row_inv(src), nrm.q_norm);
     rotate(lo, hi, P + i);
+    if (NORM_D) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        lo[j] = make_float4(lo[j].x * nrm.q_prescale, lo[j].y * nrm.q_prescale, lo[j].z * nrm.q_prescale,
+                            lo[j].w * nrm.q_prescale);
+        hi[j] = make_float4(hi[j].x * nrm.q_prescale, hi[j].y * nrm.q_prescale, hi[j].z * nrm.q_prescale,
+                            hi[j].w * nrm.q_prescale);
+      }
+    }
     bf16 *dst = qb + (i * Hq + hq) * (long)D;
     *reinterpret_cast<bf16x8 *>(dst + p0) = to_bf16(lo, qscale);
     *reinterpret_cast<bf16x8 *>(dst + half + p0) = to_bf16(hi, qscale);
@@ -399,6 +468,7 @@ __global__ __launch_bounds__(256) void prefill_append_kernel(
     load2(ks + half + p0, khi);
     load2(vs + p0, vlo);
     load2(vs + half + p0, vhi);
+    if (NORM_D) norm(klo, khi, row_inv(ks), nrm.k_norm);
     rotate(klo, khi, pos);
     float *ck = cache_k + (pos * H + h) * (long)D, *cv = cache_v + (pos * H + h) * (long)D;
     store2(ck + p0, klo);
@@ -447,14 +517,20 @@ static inline unsigned blocks_for(long n, int per) { return (unsigned)((n + per 
 hipError_t launch_prefill_append(hipStream_t st, const float *q, const float *k, const float *v,
                                  const float *cos_tab, const float *sin_tab, size_t P, size_t S, size_t H,
                                  size_t Hq, size_t D, float *cache_k, float *cache_v, bf16 *kb, bf16 *vt,
-                                 size_t cap, bf16 *qb, float qscale) {
+                                 size_t cap, bf16 *qb, float qscale, const PrefillNorm *norm) {
   if (S == 0) return hipSuccess;
   const long pad_end = ((long)(P + S) + 63) & ~63L;
   if (D % 64 != 0 || cap % 64 != 0 || pad_end > (long)cap) return hipErrorInvalidValue;
   const long kv_blocks = (pad_end - ((long)P & ~63L)) / 64, q_blocks = ((long)S + 63) / 64;
   dim3 grid((unsigned)std::max(kv_blocks, q_blocks), (unsigned)(H + Hq), (unsigned)(D / 64));
-  hipLaunchKernelGGL(prefill_append_kernel, grid, dim3(256), 0, st, q, k, v, cos_tab, sin_tab, (long)P, (long)S,
-                     (int)H, (int)Hq, (int)D, cache_k, cache_v, kb, vt, (long)cap, pad_end, qb, qscale);
+  const PrefillNorm none{};
+  auto kern = prefill_append_kernel<0>;
+  if (norm) {
+    if (D != 64 && D != 128 && D != 256) return hipErrorInvalidValue;
+    kern = D == 64 ? prefill_append_kernel<64> : D == 128 ? prefill_append_kernel<128> : prefill_append_kernel<256>;
+  }
+  hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, q, k, v, cos_tab, sin_tab, (long)P, (long)S, (int)H, (int)Hq,
+                     (int)D, cache_k, cache_v, kb, vt, (long)cap, pad_end, qb, qscale, norm ? *norm : none);
   return hipGetLastError();
 }
 

@@ -261,6 +261,15 @@ class Session:
             self.handle, None if table is None else table.handle, _dev(q, "q"), _dev(k, "k"), _dev(v, "v"),
             cache.handle, C.byref(cfg), _dev(out, "out")))
 
+    def gemma_prefill_step(self, table: RopeTable, q, k, v, cache: KvCache, config: KvAttentionConfig, q_norm,
+                           k_norm, eps: float, q_prescale: float, out) -> None:
+        """The Gemma 3 prefill step (spissa_gemma_prefill_step_device): QK-norm, Gemma
+        RoPE, q *= q_prescale, attention and append of a chunk; q/k/v read-only."""
+        cfg = config._c()
+        check(self._lib.spissa_gemma_prefill_step_device(
+            self.handle, table.handle, _dev(q, "q"), _dev(k, "k"), _dev(v, "v"), cache.handle, C.byref(cfg),
+            _dev(q_norm, "q_norm"), _dev(k_norm, "k_norm"), float(eps), float(q_prescale), _dev(out, "out")))
+
     def attention_cached(self, q, cache: KvCache, config: KvAttentionConfig, out) -> None:
         """Append-first attention (spissa_attention_cached_device): the chunk's
         rows are already the cache's last config.query_len rows."""

@@ -186,3 +186,94 @@ def test_append_first_attention_ignores_stale_rows_past_the_cache(gpu):
     got = out.cpu().numpy()
     assert np.all(np.isfinite(got))
     assert rel_err(got, want) <= BF16_TOL
+
+
+GEMMA_CASES = [  # name, S, P, Hq, Hkv, D, window, base, divisor, query_pre_attn_scalar
+    ("gemma-1B global prefill 300, divisor 8", 300, 0, 4, 1, 256, 0, 1000000.0, 8.0, 256.0),
+    ("gemma-4B local chunk 128 on 1000 W1024", 128, 1000, 8, 4, 256, 1024, 10000.0, 1.0, 256.0),
+    ("prescale != 1, chunk 77 on 129", 77, 129, 8, 4, 256, 0, 10000.0, 1.0, 224.0),
+    ("head_dim 128, 65 rows", 65, 0, 8, 2, 128, 0, 10000.0, 1.0, 128.0),
+    ("head_dim 64, chunk 130 on 7", 130, 7, 6, 2, 64, 0, 10000.0, 1.0, 64.0),
+]
+
+
+@pytest.mark.parametrize("name,S,P,Hq,Hkv,D,W,base,div,qpas", GEMMA_CASES, ids=[c[0] for c in GEMMA_CASES])
+def test_gemma_prefill_step_matches_prologue_then_step(gpu, name, S, P, Hq, Hkv, D, W, base, div, qpas):
+    """spissa_gemma_prefill_step_device against the unfused device sequence
+    (spissa_gemma_qk_prologue_device in place on copies, then the prefill step
+    without RoPE): output and cache bitwise equal (the 1/rms pass sums the
+    squares in index order, as the prologue does); against the oracle's
+    prologue + SDPA (output <= 1e-2) and its cache after the append (bitwise)."""
+    import torch
+
+    from spissa_amd import _ffi
+    from spissa_amd.device import Session
+    from spissa_amd.rotary import KvAttentionConfig
+    from spissa_amd.synth import normal_f32, seed_for
+
+    print(f"[case] gemma prefill step {name}", flush=True)
+    eps = 1e-6
+    pre = float(np.float32(np.float32(1.0) / np.sqrt(np.float32(qpas))) * np.sqrt(np.float32(D)))
+    q, k, v, pk, pv = layer_inputs(52, D, S, P, Hq, Hkv, D)
+    qn = normal_f32(seed_for(52, D, 0, "qnorm"), D, 1.0, 0.1)
+    kn = normal_f32(seed_for(52, D, 0, "knorm"), D, 1.0, 0.1)
+    if P:
+        dummy = np.zeros(P * D, dtype=np.float32)
+        o.gemma_qk_prologue(dummy, pk, P, 1, Hkv, D, qn, kn, eps, base, div, 0, qpas)
+    ref = o.KvCache(Hkv, D, P + S)
+    if P:
+        ref.append(pk, pv, P)
+    rq, rk = q.copy(), k.copy()
+    o.gemma_qk_prologue(rq, rk, S, Hq, Hkv, D, qn, kn, eps, base, div, P, qpas)
+    want = o.sdpa_with_cache(rq, rk, v, ref, S, Hq, Hkv, D, True, W)
+    ref.append(rk, v, S)
+
+    s = Session(0)
+    table = s.rope_table(_ffi.ROPE_GEMMA, D, base, position_divisor=div, max_positions=P + S + 8)
+    fused, unfused = s.kv_cache(Hkv, D, P + S), s.kv_cache(Hkv, D, P + S)
+    if P:
+        fused.append(pk, pv, P)
+        unfused.append(pk, pv, P)
+    cfg = KvAttentionConfig(S, Hq, Hkv, D, True, W)
+    dq, dk, dv, dqn, dkn = (torch.from_numpy(x).cuda() for x in (q, k, v, qn, kn))
+    out = torch.empty_like(dq)
+    s.gemma_prefill_step(table, dq, dk, dv, fused, cfg, dqn, dkn, eps, pre, out)
+    uq, uk = dq.clone(), dk.clone()
+    s.gemma_qk_prologue(table, uq, uk, S, Hq, Hkv, D, dqn, dkn, eps, P, pre)
+    uout = torch.empty_like(dq)
+    s.prefill_step(None, uq, uk, dv, unfused, cfg, uout)
+    s.sync()
+    got = out.cpu().numpy()
+    assert np.array_equal(dq.cpu().numpy(), q) and np.array_equal(dk.cpu().numpy(), k), "inputs are read-only"
+    assert_bitwise(got, uout.cpu().numpy(), "output: fused vs prologue + step")
+    assert_bitwise(fused.keys(), unfused.keys(), "keys: fused vs prologue + step")
+    assert rel_err(got, want) <= BF16_TOL
+    assert fused.len() == P + S
+    assert_bitwise(fused.keys(), ref.keys(), "keys against the oracle")
+    assert_bitwise(fused.values(), ref.values(), "values against the oracle")
+
+
+def test_gemma_prefill_step_checks_its_arguments(gpu):
+    import torch
+
+    from spissa_amd import _ffi
+    from spissa_amd.device import Session
+    from spissa_amd.rotary import KvAttentionConfig
+
+    Hq, Hkv, D, S = 4, 1, 256, 8
+    s = Session(0)
+    llama = s.rope_table(_ffi.ROPE_LLAMA, D, 10000.0, max_positions=64)
+    gemma = s.rope_table(_ffi.ROPE_GEMMA, D, 10000.0, position_divisor=1.0, max_positions=64)
+    cache = s.kv_cache(Hkv, D, 12)
+    cfg = KvAttentionConfig(S, Hq, Hkv, D, True)
+    q = torch.zeros(S * Hq * D, device="cuda")
+    k = torch.zeros(S * Hkv * D, device="cuda")
+    w = torch.ones(D, device="cuda")
+    out = torch.empty_like(q)
+    with pytest.raises(gpu.ArgumentError):  # a llama table
+        s.gemma_prefill_step(llama, q, k, k, cache, cfg, w, w, 1e-6, 1.0, out)
+    s.gemma_prefill_step(gemma, q, k, k, cache, cfg, w, w, 1e-6, 1.0, out)
+    with pytest.raises(gpu.ShapeError):  # 8 more rows exceed the capacity of 12: nothing runs
+        s.gemma_prefill_step(gemma, q, k, k, cache, cfg, w, w, 1e-6, 1.0, out)
+    s.sync()
+    assert cache.len() == 8
