@@ -1888,15 +1888,27 @@ extern "C" int spissa_attention_sublayer_device(spissa_session *s, const spissa_
     float *const oqkv[3] = {q, k, v};
     ST_TRY(linear_launch_multi(s, wqkv, xn, S, oqkv, 3));
   }
-  if (qk_norm)
-    ST_TRY(spissa_gemma_qk_prologue_device(s, L->rope, q, k, S, Hq, Hkv, D, L->d_q_norm, L->d_k_norm, L->eps, pos,
-                                           L->q_prescale));
   if (S == 1 && cache && decode_supported((int)D, (int)(Hq / Hkv)) && decode_cache_fits(cache)) {
-    // RoPE (Llama), attention and append in the fused decode step
+    // (QK-norm,) RoPE, attention and append in the fused decode step
     spissa_kv_cache *caches[1] = {cache};
-    ST_TRY(spissa_decode_step_device(s, qk_norm ? nullptr : L->rope, q, k, v, caches, 1, &cfg, att));
+    if (qk_norm)
+      ST_TRY(spissa_gemma_decode_step_device(s, L->rope, q, k, v, caches, 1, &cfg, L->d_q_norm, L->d_k_norm, L->eps,
+                                             L->q_prescale, att));
+    else
+      ST_TRY(spissa_decode_step_device(s, L->rope, q, k, v, caches, 1, &cfg, att));
+  } else if (S > 1 && cache && prefill_supported((int)D) && s->prefill_precision == SPISSA_PREFILL_BF16) {
+    // (QK-norm,) RoPE, append and attention in the fused prefill step
+    if (qk_norm)
+      ST_TRY(spissa_gemma_prefill_step_device(s, L->rope, q, k, v, cache, &cfg, L->d_q_norm, L->d_k_norm, L->eps,
+                                              L->q_prescale, att));
+    else
+      ST_TRY(spissa_prefill_step_device(s, L->rope, q, k, v, cache, &cfg, att));
   } else {
-    if (!qk_norm && L->rope) ST_TRY(spissa_rope_apply_device(s, L->rope, q, k, S, Hq, Hkv, D, pos));
+    if (qk_norm)
+      ST_TRY(spissa_gemma_qk_prologue_device(s, L->rope, q, k, S, Hq, Hkv, D, L->d_q_norm, L->d_k_norm, L->eps, pos,
+                                             L->q_prescale));
+    else if (L->rope)
+      ST_TRY(spissa_rope_apply_device(s, L->rope, q, k, S, Hq, Hkv, D, pos));
     ST_TRY(spissa_attention_device(s, q, k, v, cache, &cfg, att));
     if (cache) ST_TRY(spissa_kv_cache_append_device(cache, k, v, S));
   }
