@@ -1120,10 +1120,18 @@ static void plan_prefill(PrefillArgs &a, int D, int cus, PrefillPlan *p) {
       p->ppart_bytes = (size_t)a.splits * S * a.Hq * (D + 2) * sizeof(float);
     }
   }
-  // The O split where a workgroup covers at least 32 key tiles (measured:
-  // 10% faster on a 4096-token causal prefill at head_dim 256, 5-9% slower on
-  // windowed and split ranges of 10-19 tiles).
-  a.o_split = D >= 256 && (a.splits > 1 ? a.tps : p->tiles) >= 32;
+  // head_dim 256: the O split (two waves per (head, query block), each with
+  // half the score and output MFMAs) where a workgroup covers at least 8 key
+  // tiles. Windowed layers with at least one workgroup per two CUs run it
+  // unsplit: the key-split combine costs more than the CUs left idle
+  // (measured on Gemma-3-1B's W512 layer: 42.8 against 46.6 us).
+  a.o_split = D >= 256 && (a.splits > 1 ? a.tps : p->tiles) >= 8;
+  if (D >= 256 && a.window > 0 && base * 2 >= cus) {
+    a.splits = 1;
+    a.tps = 0;
+    p->ppart_bytes = 0;
+    a.o_split = 1;
+  }
   a.xcd_group = prefill_use_xcd_group(a, D) ? 1 : 0;
   const int wgq = prefill_wg_queries(a, D);
   p->workgroups = (size_t)prefill_grid_workgroups((S + wgq - 1) / wgq, a.R / (128 / wgq), a.Hkv, a.splits,

@@ -133,10 +133,9 @@ struct Geom {
 // [T0, T1): the first step starts from the row bias (BIAS: every element of
 // bias[qb] is minus the row's exponent reference) or from s (a masked tile's
 // start, already in s); later ones accumulate; kbuf is the K tile in LDS.
-template <int D, int BN, int QB, int T0, int T1, bool BIAS>
-__device__ __forceinline__ void score_tile(f32x16 (&s)[QB][BN / 32], const char *kbuf,
-                                           const unsigned (&k_rd)[D / 16],
-                                           const bf16x8 (&qf)[QB][D / 16], const f32x16 (&bias)[QB]) {
+template <int D, int BN, int QB, int T0, int T1, bool BIAS, int NT>
+__device__ __forceinline__ void score_tile(f32x16 (&s)[QB][BN / 32], const char *kbuf, const unsigned (&k_rd)[NT],
+                                           const bf16x8 (&qf)[QB][NT], const f32x16 (&bias)[QB]) {
   constexpr int KB = BN / 32;
 #pragma unroll
   for (int tt = T0; tt < T1; ++tt)
@@ -166,9 +165,12 @@ __device__ __forceinline__ float sum_bf16x8(const bf16x8 p) {
 // QB query blocks of 32 per wave (1 or 2); two waves per SIMD unless the
 // accumulators need the whole register file (two 128-wide blocks).
 // OS: waves sharing one (head, query block), each holding D / OS columns of
-// O. With OS = 2 both compute the whole score tile and each accumulates its
-// half of O^T += V^T P^T: 1.5x the MFMAs, but half the O registers, which at
-// head_dim 256 lets two waves share a SIMD instead of one.
+// Q and O. With OS = 2 each wave computes the partial scores of its half of
+// the head dims; the two partials are exchanged through LDS and added in a
+// fixed order (the half with the exponent bias first), so both waves hold
+// the same score tile and the same softmax state, and each accumulates its
+// half of O^T += V^T P^T. Half the O and Q registers lets two waves share a
+// SIMD at head_dim 256, with no MFMA done twice.
 template <int D, int RB, int NPB, int BN, int QB, int OS>
 __global__ __launch_bounds__(RB *NPB *OS * 64, (OS == 1 && ((QB == 1 && D <= 128) || D <= 64)) ? 2 : 1) void
 prefill_kernel(const PrefillArgs a) {
@@ -181,6 +183,8 @@ prefill_kernel(const PrefillArgs a) {
   // at head_dim 128, eagerly 4-5% faster at 64 and 256.
   constexpr bool LAZY = D == 128;
   constexpr int DT = G::DT, KB = G::KB, KS = G::KS, DB = G::DB / OS;  // DB: output blocks of this wave
+  constexpr int DTW = DT / OS;  // 16-dim score steps of this wave
+  static_assert(OS == 1 || (OS == 2 && !LAZY), "the score exchange runs with the eager reference");
 
   // Four separate LDS objects (not one array): the compiler then knows that
   // copies into one buffer do not alias reads of another and does not wait
@@ -189,6 +193,8 @@ prefill_kernel(const PrefillArgs a) {
   __shared__ __attribute__((aligned(1024))) char k_lds1[G::KBYTES];
   __shared__ __attribute__((aligned(1024))) char v_lds0[G::VBYTES];
   __shared__ __attribute__((aligned(1024))) char v_lds1[G::VBYTES];
+  // OS = 2: partial score tiles, two slots per wave (a 4-KB placeholder otherwise)
+  __shared__ __attribute__((aligned(16))) float s_x[2][OS == 2 ? NW : 1][OS == 2 ? QB * KB * 4 : 1][64][4];
 
   const int HB = a.R / RB;
   int h, hb, split, qt;
@@ -251,19 +257,19 @@ prefill_kernel(const PrefillArgs a) {
   // Q carries the softmax scale times log2(e), so the scores come out of the
   // MFMAs in the log2 domain.
   const float c = a.qk_scale_log2;
-  bf16x8 qf[QB][DT];
+  bf16x8 qf[QB][DTW];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     const int pos = min(wp0 + 32 * qb + lq, a.S - 1);
     if (a.qb) {  // already scaled and rounded (the fused prefill step)
-      const bf16 *qp = a.qb + ((long)pos * a.Hq + head) * D + 8 * hl;
+      const bf16 *qp = a.qb + ((long)pos * a.Hq + head) * D + oh * (D / OS) + 8 * hl;
 #pragma unroll
-      for (int t = 0; t < DT; ++t) qf[qb][t] = *reinterpret_cast<const bf16x8 *>(qp + 16 * t);
+      for (int t = 0; t < DTW; ++t) qf[qb][t] = *reinterpret_cast<const bf16x8 *>(qp + 16 * t);
       continue;
     }
-    const float *qp = a.q + ((long)pos * a.Hq + head) * D + 8 * hl;
+    const float *qp = a.q + ((long)pos * a.Hq + head) * D + oh * (D / OS) + 8 * hl;
 #pragma unroll
-    for (int t = 0; t < DT; ++t) {
+    for (int t = 0; t < DTW; ++t) {
       const float4 x0 = *reinterpret_cast<const float4 *>(qp + 16 * t);
       const float4 x1 = *reinterpret_cast<const float4 *>(qp + 16 * t + 4);
       bf16x8 v;
@@ -286,9 +292,9 @@ prefill_kernel(const PrefillArgs a) {
 
   // LDS byte offsets of this lane's fragments (key block 0 / dim block 0).
   // (Rows of a fragment are 32 * block + lq, and 32 * block leaves swz unchanged.)
-  unsigned k_rd[DT], v_rd[KS];
+  unsigned k_rd[DTW], v_rd[KS];
 #pragma unroll
-  for (int t = 0; t < DT; ++t) k_rd[t] = lq * 2 * D + 16 * ((2 * t + hl) ^ swz<G::KNC>(lq));
+  for (int t = 0; t < DTW; ++t) k_rd[t] = lq * 2 * D + 16 * ((2 * (oh * DTW + t) + hl) ^ swz<G::KNC>(lq));
 #pragma unroll
   for (int t = 0; t < KS; ++t) v_rd[t] = lq * 2 * BN + 16 * ((2 * t + hl) ^ swz<G::VNC>(lq));
 
@@ -373,7 +379,8 @@ prefill_kernel(const PrefillArgs a) {
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             const int kk = kb * 32 + 8 * (i >> 2) + (i & 3);
-            s[qb][kb][i] = (kk < lo || kk > hi) ? NEG_INF : -ms[qb];
+            // (with OS = 2 the mask and the bias go into the first half's partial)
+            s[qb][kb][i] = oh != 0 ? 0.0f : (kk < lo || kk > hi) ? NEG_INF : -ms[qb];
           }
       }
       score_tile<D, BN, QB, 0, 1, false>(s, kbuf, k_rd, qf, bias);
@@ -394,6 +401,38 @@ prefill_kernel(const PrefillArgs a) {
     }
   };
 
+  // OS = 2: the partial score tile of tile t goes to LDS slot t & 1 (a lane's
+  // 16 scores of block (qb, kb) as four float4 rows of 64 lanes, conflict-free);
+  // after the next barrier the partner wave adds it to its own partial, the
+  // first half's partial (which holds the bias and the mask) first.
+  auto put_scores = [&](const f32x16 (&s)[QB][KB], int t) {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<float4 *>(&s_x[t & 1][wave][(qb * KB + kb) * 4 + g][lane][0]) =
+              make_float4(s[qb][kb][4 * g], s[qb][kb][4 * g + 1], s[qb][kb][4 * g + 2], s[qb][kb][4 * g + 3]);
+  };
+  auto add_partner_scores = [&](f32x16 (&s)[QB][KB], int t) {
+    const int partner = (wave + RB * NPB) % NW;
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const float4 p = *reinterpret_cast<const float4 *>(&s_x[t & 1][partner][(qb * KB + kb) * 4 + g][lane][0]);
+          const float pv[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float own = s[qb][kb][4 * g + i];
+            s[qb][kb][4 * g + i] = oh == 0 ? own + pv[i] : pv[i] + own;
+          }
+        }
+  };
+
   // One pipelined step on tile t (scores in `cur`, exponent reference ms
   // already covering tile t, O and l already scaled to it):
   //   copies of K(t+2) and V(t+1) go out;
@@ -406,6 +445,40 @@ prefill_kernel(const PrefillArgs a) {
   // O selects the buffers.
   auto step = [&](auto O_, int t, f32x16 (&cur)[QB][KB], f32x16 (&nxt)[QB][KB]) {
     constexpr int O = decltype(O_)::value;
+    if constexpr (OS == 2) {
+      // The whole score tile t (the partner's half arrived at the last
+      // barrier), then the eager reference check on it, before its
+      // exponentials and before the bias of S(t+1) is used.
+      if (t != t_begin) {
+        add_partner_scores(cur, t);
+        float mx[QB];
+        row_max(cur, mx);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          const bool raise = mx[qb] > m[qb] + kRescaleSlack;
+          if (__ballot(raise)) {
+            const float mnew = raise ? mx[qb] : m[qb];
+            const float msn = mnew == NEG_INF ? 0.0f : mnew;
+            const float alpha = fast_exp2(m[qb] - msn), shift = msn - ms[qb];
+            l[qb] *= alpha;
+#pragma unroll
+            for (int d = 0; d < DB; ++d)
+#pragma unroll
+              for (int i = 0; i < 16; ++i) oacc[qb][d][i] *= alpha;
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+              for (int i = 0; i < 16; ++i) cur[qb][kb][i] -= shift;
+            m[qb] = mnew;
+            ms[qb] = msn;
+            if (oh == 0) {
+#pragma unroll
+              for (int i = 0; i < 16; ++i) bias[qb][i] = -ms[qb];
+            }
+          }
+        }
+      }
+    }
     char *const k_this = O ? k_lds1 : k_lds0;  // receives K(t+2)
     char *const k_next = O ? k_lds0 : k_lds1;  // holds K(t+1)
     char *const v_this = O ? v_lds1 : v_lds0;  // holds V(t)
@@ -431,7 +504,8 @@ prefill_kernel(const PrefillArgs a) {
         pf[qb][ks] = p;
       }
     }
-    score_tile<D, BN, QB, 1, DT, false>(nxt, k_next, k_rd, qf, bias);
+    score_tile<D, BN, QB, 1, DTW, false>(nxt, k_next, k_rd, qf, bias);
+    if constexpr (OS == 2) put_scores(nxt, t + 1);
 
     if constexpr (LAZY) {
     // The exponent reference is raised lazily: only a row whose probabilities
@@ -495,7 +569,7 @@ prefill_kernel(const PrefillArgs a) {
         for (int qb = 0; qb < QB; ++qb)
           oacc[qb][d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[qb][ks], oacc[qb][d], 0, 0, 0);
       }
-    if constexpr (!LAZY) {
+    if constexpr (!LAZY && OS == 1) {
     const bool has_next = t + 1 < t_end;
     float mx[QB], alpha[QB], shift[QB];
     bool raise[QB];
@@ -548,7 +622,12 @@ prefill_kernel(const PrefillArgs a) {
     for (int i = 0; i < 16; ++i) bias[qb][i] = 0.0f;
   }
   score_first(sa, k_lds0, t_begin);
-  score_tile<D, BN, QB, 1, DT, false>(sa, k_lds0, k_rd, qf, bias);
+  score_tile<D, BN, QB, 1, DTW, false>(sa, k_lds0, k_rd, qf, bias);
+  if constexpr (OS == 2) {
+    put_scores(sa, t_begin);
+    __syncthreads();
+    add_partner_scores(sa, t_begin);
+  }
   {
     float mx[QB];
     row_max(sa, mx);
@@ -560,8 +639,10 @@ prefill_kernel(const PrefillArgs a) {
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) sa[qb][kb][i] -= ms[qb];
+      if (oh == 0) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) bias[qb][i] = -ms[qb];
+        for (int i = 0; i < 16; ++i) bias[qb][i] = -ms[qb];
+      }
     }
   }
   __syncthreads();  // every wave is done with K(t0) before K(t0+2) lands in its buffer
