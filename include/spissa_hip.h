@@ -265,7 +265,8 @@ typedef struct {
     int heads_per_block;    /* decode: query heads sharing one K/V read */
     int head_blocks;        /* decode: head blocks per KV head */
     int keys_per_split;     /* decode: cached keys per split workgroup */
-    int splits;             /* decode: splits of the longest sequence; prefill: key splits (1: none) */
+    int splits;             /* decode: splits of the longest sequence, the token's own included; prefill: key splits (1: none) */
+    int token_split;        /* decode: the new token has a split of its own after the cached keys' (else split 0 takes it) */
     int tiles_per_split;    /* prefill with key splits: key tiles per split */
     int tile_keys;          /* prefill: keys per tile */
     int workgroup_queries;  /* prefill: queries per workgroup */

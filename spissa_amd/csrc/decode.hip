@@ -174,11 +174,15 @@ __global__ __launch_bounds__(256, 4) void decode_split_kernel(const DecodeArgs a
   const int b = blockIdx.z;
   const int P = a.seq[b].past;
   const int kstart = a.window > 0 ? max(0, P + 1 - a.window) : 0;
-  // The cached keys in splits of kps; split 0 also takes the new token (one
-  // split with no cached key when there are none).
-  const int nsplit = max(1, (P - kstart + a.kps - 1) / a.kps);
+  // The cached keys in splits of kps. The new token has a split of its own,
+  // split 0, dispatched first (tok_split; the cached splits are then 1..),
+  // or is taken by cached split 0 (one split with no cached key when there
+  // are none).
+  const int ncached = (P - kstart + a.kps - 1) / a.kps;
+  const int nsplit = a.tok_split ? ncached + 1 : max(1, ncached);
   if (split >= nsplit) return;
-  const int k0 = kstart + split * a.kps;
+  const int cs = a.tok_split ? split - 1 : split;  // cached split index (-1: the token's own)
+  const int k0 = cs < 0 ? P : kstart + cs * a.kps;
   const int k1 = min(P, k0 + a.kps);
 
   const int tid = threadIdx.x;
@@ -296,10 +300,11 @@ __global__ __launch_bounds__(256, 4) void decode_split_kernel(const DecodeArgs a
     }
   }
 
-  // ---- the new token (key P), in split 0: wave 0 adds it as one more row.
+  // ---- the new token (key P), in its own split or in split 0: wave 0 adds
+  // it as one more row.
   // Every row group of the wave loads the same row, so its scores are
   // uniform and only group 0 adds the value. ----
-  if (split == 0 && wave == 0) {
+  if ((a.tok_split ? cs < 0 : cs == 0) && wave == 0) {  // the token's own split, or cached split 0
     const long row = ((long)b * a.Hkv + h) * D;
     float4 kn0 = ld4(a.cur_k + row + 4 * sub), kn1 = ld4(a.cur_k + row + HALF + 4 * sub);
     const float4 vn0 = ld4(a.cur_v + row + 4 * sub), vn1 = ld4(a.cur_v + row + HALF + 4 * sub);
@@ -419,7 +424,8 @@ __global__ __launch_bounds__(1024) void decode_combine_kernel(const DecodeArgs a
   const int b = blockIdx.z;
   const int P = a.seq[b].past;
   const int kstart = a.window > 0 ? max(0, P + 1 - a.window) : 0;
-  const int nsplit = max(1, (P - kstart + a.kps - 1) / a.kps);
+  const int ncached = (P - kstart + a.kps - 1) / a.kps;
+  const int nsplit = a.tok_split ? ncached + 1 : max(1, ncached);
   const int tid = threadIdx.x;
   const int out = tid & (OUTS - 1);
   const int sl = tid / OUTS;
@@ -532,7 +538,7 @@ int decode_keys_per_split(int D, int RB, long total_rows, int max_keys, int spli
   const int chunk = 4 * (64 / (D / 8)) * rows_per_group(RB);  // keys of one workgroup iteration
   // about 1024 workgroups over the launch (grids of exactly 3 or 4 per CU
   // measured no faster)
-  constexpr long target = 1024;
+  constexpr long target = kDecodeRoundWorkgroups;
   const long per = (total_rows + target - 1) / target;
   long kps = ((per + chunk - 1) / chunk) * chunk;
   if (kps < chunk) kps = chunk;

@@ -20,6 +20,9 @@ enum : int { kDevErrSoftmaxDenominator = 1 };
 constexpr int kMaxDecodeBatch = 16;
 // Most key splits of one (sequence, KV head) the decode combine reads.
 constexpr int kMaxDecodeSplits = 512;
+// Workgroups of one round of the decode split kernel (4 per CU on 256 CUs),
+// the size decode_keys_per_split aims the grid at.
+constexpr int kDecodeRoundWorkgroups = 1024;
 // Prefill key tiles are at most this wide; the staging buffer starts at a
 // multiple of it.
 constexpr int kPrefillTileAlign = 64;
@@ -69,7 +72,11 @@ struct DecodeArgs {
   int B, Hq, Hkv, R, HB;  // R = Hq/Hkv, HB = head blocks per kv head
   int window;
   int kps;             // cached keys per split
-  int max_splits;      // splits of the longest sequence in the launch
+  int max_splits;      // splits of the longest sequence in the launch (with the token's own)
+  // 1: the new token is a split of its own after the cached keys' (its
+  // latency -- loads, QK-norm, RoPE, append -- then overlaps the streaming
+  // splits); 0: split 0 takes it after its cached rows.
+  int tok_split;
   float qscale;        // softmax scale * log2(e), applied to the scores
   SeqDesc seq[kMaxDecodeBatch];
 };

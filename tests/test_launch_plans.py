@@ -30,8 +30,10 @@ TILE_ALIGN = 64
 def check_decode(cfg, past, plan, noalloc=False):
     """decode_split_kernel: grid (Hkv*HB, max_splits, B); split s of sequence b
     covers cached keys [kstart + s*kps, min(P, kstart + (s+1)*kps)) where
-    kstart = max(0, P + 1 - W) with a window; the first of its
-    max(1, ceil((P - kstart) / kps)) splits also takes the new token (key P)."""
+    kstart = max(0, P + 1 - W) with a window, for s < ceil((P - kstart) / kps);
+    with token_split the new token (key P) is split 0 of its own (dispatched
+    first) and cached split s is grid split s + 1, else cached split 0 takes
+    it (one split at least)."""
     D, Hq, Hkv, W = cfg.head_dim, cfg.num_heads, cfg.kv_heads, cfg.window
     assert plan["path"] == _ffi.KERNEL_DECODE
     RB, HB, kps = plan["heads_per_block"], plan["head_blocks"], plan["keys_per_split"]
@@ -49,13 +51,17 @@ def check_decode(cfg, past, plan, noalloc=False):
     for b in range(B):
         P = past[b]
         kstart = max(0, P + 1 - W) if W > 0 else 0
-        nsplit = max(1, -(-(P - kstart) // kps))
+        ncached = -(-(P - kstart) // kps)
+        nsplit = ncached + 1 if plan["token_split"] else max(1, ncached)
         assert nsplit <= max_splits
         covered = []
         for s in range(nsplit):
-            k0 = kstart + s * kps
+            cs = s - 1 if plan["token_split"] else s
+            if cs < 0:
+                continue  # the token's own split reads no cached row
+            k0 = kstart + cs * kps
             k1 = min(P, k0 + kps)
-            assert k0 < k1 or (s == 0 and P == kstart)  # split 0 holds at least the new token
+            assert k0 < k1 or (cs == 0 and P == kstart)  # cached split 0 holds at least the new token
             covered.append((k0, k1))
             for h in range(Hkv):
                 for hb in range(HB):
@@ -192,6 +198,18 @@ def test_decode_plan_covers_every_key(name, Hq, Hkv, D, past, W, noalloc):
     assert plan["partial_bytes"] >= max(
         plan_attention(cfg, past[b0:b0 + MAX_DECODE_BATCH], noalloc=noalloc)["partial_bytes"]
         for b0 in range(0, len(past), MAX_DECODE_BATCH))
+
+
+def test_decode_token_split_only_when_two_entries_fit():
+    cfg = KvAttentionConfig(1, 24, 8, 128, True, 0)
+    assert plan_attention(cfg, [8192])["token_split"] == 1
+    assert plan_attention(cfg, [8192], noalloc=True)["token_split"] == 1
+    # batch 16: the grid already fills a round of workgroup slots
+    assert plan_attention(cfg, [8192] * 16)["token_split"] == 0
+    # 15 sequences x 512 heads x (256 + 2) floats fill the scratch array once: the token goes to split 0
+    wide = KvAttentionConfig(1, 512, 512, 256, True, 0)
+    plan = plan_attention(wide, [4] * 15, noalloc=True)
+    assert plan["token_split"] == 0 and plan["splits"] == 1
 
 
 def test_noalloc_plan_coarsens_splits_to_the_scratch_array():
