@@ -129,6 +129,30 @@ def read_ceiling(sess, stream, dev) -> dict:
     return out
 
 
+def mfma_ceiling(sess, stream, dev) -> dict:
+    """The library's dense-MFMA kernel (spissa_mfma_rate_probe_device: eight
+    waves per CU issuing independent v_mfma_f32_32x32x16_bf16 from registers,
+    no memory traffic), about 1 ms per launch; event-timed over 10 launches on
+    the session stream after one warm-up. The rate it sustains, with the
+    chip's clock and power limits, is the achievable bound of the prefill
+    kernels beside the 2.5 PFLOP/s spec."""
+    import torch
+
+    sink = torch.zeros(1, dtype=torch.float32, device=dev)
+    rounds = 4096
+    flop = sess.mfma_rate_probe(rounds, sink)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(10):
+        sess.mfma_rate_probe(rounds, sink)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / 10
+    tf = flop / (ms * 1e-3) / 1e12
+    return {"us": round(ms * 1e3, 2), "flop": flop, "TFLOPs": round(tf, 1), "frac_of_spec": round(tf / BF16_PEAK_TFLOPS, 4)}
+
+
 def gpu_bench(args) -> dict:
     import torch
 
@@ -148,6 +172,7 @@ def gpu_bench(args) -> dict:
 
     with torch.cuda.stream(stream):
         res["hbm_read_ceiling"] = read_ceiling(sess, stream, dev)
+        res["mfma_ceiling"] = mfma_ceiling(sess, stream, dev)
 
         # ---- decode, batch 1 ----
         log("filling 28 layer caches (8192 tokens each)")
@@ -1095,6 +1120,7 @@ def main() -> int:
                       "event-timed average over 28 back-to-back launches per graph replay",
         },
         "hbm_read_ceiling": res.get("hbm_read_ceiling"),
+        "mfma_ceiling": res.get("mfma_ceiling"),
         "device": res.get("device"),
     }
     if "decode_b16" in res:
@@ -1113,6 +1139,9 @@ def main() -> int:
         line["roofline_prefill"] = {"bound": "mfma", "achieved": round(p["TFLOPs"], 2), "peak": BF16_PEAK_TFLOPS,
                                     "unit": "TFLOP/s", "frac": round(p["TFLOPs"] / BF16_PEAK_TFLOPS, 4),
                                     "dtype": "bf16 MFMA, f32 accumulate"}
+        if res.get("mfma_ceiling"):
+            line["roofline_prefill"]["frac_of_measured_ceiling"] = round(
+                p["TFLOPs"] / res["mfma_ceiling"]["TFLOPs"], 4)
     if "sublayer_b1" in res:
         line["sublayer_b1"] = {"workload": "llama-3.2-3B attention sublayer at decode, batch 1, 8192-token "
                                            "cache: input RMSNorm, q/k/v projections (bf16), RoPE + attention "

@@ -443,6 +443,14 @@ int spissa_attention_sublayer_device(spissa_session *s, const spissa_attention_l
  * d_buf 16-byte aligned, bytes a multiple of 16 (SHAPE otherwise); d_sink is
  * one float the kernel may write. */
 int spissa_hbm_read_probe_device(spissa_session *s, const void *d_buf, size_t bytes, float *d_sink);
+/* Dense bf16 MFMA ceiling (no reference counterpart): two four-wave
+ * workgroups per CU, each wave issuing rounds x 8 independent
+ * v_mfma_f32_32x32x16_bf16 from registers, asynchronously on the session
+ * stream; *flop receives the launch's FLOP count (host pointer). Timing it
+ * gives the MFMA rate the device sustains, clock and power limits included,
+ * which the prefill figures are compared with. rounds > 0 (SHAPE otherwise);
+ * d_sink is one float the kernel may write. */
+int spissa_mfma_rate_probe_device(spissa_session *s, int rounds, float *d_sink, double *flop);
 
 /* Prefill arithmetic for query_len > 1: SPISSA_PREFILL_BF16 (default) runs
  * the MFMA kernel; SPISSA_PREFILL_F32 runs the f32 SIMT kernel. */

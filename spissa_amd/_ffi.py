@@ -176,6 +176,7 @@ SIGNATURES = {
         [C.POINTER(AttnConfigC), C.POINTER(c_size), c_size, C.c_int, C.c_int, C.c_int,
          C.POINTER(AttentionPlanC)]),
     "spissa_hbm_read_probe_device": (C.c_int, [c_void_p, c_void_p, c_size, c_void_p]),
+    "spissa_mfma_rate_probe_device": (C.c_int, [c_void_p, C.c_int, c_void_p, C.POINTER(C.c_double)]),
     "spissa_gemma_prefill_step_device": (
         C.c_int,
         [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, C.POINTER(AttnConfigC), c_void_p, c_void_p,

@@ -290,6 +290,16 @@ extern "C" int spissa_hbm_read_probe_device(spissa_session *s, const void *d_buf
   GUARD_END
 }
 
+extern "C" int spissa_mfma_rate_probe_device(spissa_session *s, int rounds, float *d_sink, double *flop) {
+  GUARD_BEGIN
+  if (!s || !d_sink || !flop) return set_err(SPISSA_ERR_ARGUMENT, "null argument");
+  if (rounds <= 0) return set_err(SPISSA_ERR_SHAPE, "the MFMA probe needs rounds > 0, got %d", rounds);
+  HIP_TRY(hipSetDevice(s->device));
+  HIP_TRY(launch_mfma_rate(s->stream, s->cus, rounds, d_sink, flop));
+  return SPISSA_OK;
+  GUARD_END
+}
+
 extern "C" int spissa_session_set_prefill_precision(spissa_session *s, int precision) {
   if (!s) return set_err(SPISSA_ERR_ARGUMENT, "session is null");
   if (precision != SPISSA_PREFILL_BF16 && precision != SPISSA_PREFILL_F32)

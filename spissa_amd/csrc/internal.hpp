@@ -190,6 +190,9 @@ hipError_t launch_stage_bf16(hipStream_t st, const float *k_rows, const float *v
                              size_t dst_first, size_t dst_cap);
 hipError_t launch_decode(hipStream_t st, const DecodeArgs &a, int D, int RB);
 // Streaming-read probe: reads bytes (a multiple of 16, 16-byte aligned) of buf once.
+// The dense bf16 MFMA ceiling: rounds x 8 MFMAs on each of 8 waves per CU;
+// *flop receives the launch's FLOP count.
+hipError_t launch_mfma_rate(hipStream_t st, int cus, int rounds, float *sink, double *flop);
 hipError_t launch_hbm_read(hipStream_t st, const void *buf, size_t bytes, float *sink);
 hipError_t launch_prefill(hipStream_t st, const PrefillArgs &a, int D);
 // Merges the key splits of a split prefill into `out` (and the error flag).

@@ -285,6 +285,13 @@ class Session:
         check(self._lib.spissa_hbm_read_probe_device(self.handle, buf.data_ptr(),
                                                      buf.numel() * buf.element_size(), _dev(sink, "sink")))
 
+    def mfma_rate_probe(self, rounds: int, sink) -> float:
+        """Launches the dense-MFMA ceiling kernel (rounds x 8 MFMAs per wave, eight
+        waves per CU); returns the launch's FLOP count. `sink`: one float32 on the device."""
+        flop = C.c_double()
+        check(self._lib.spissa_mfma_rate_probe_device(self.handle, int(rounds), _dev(sink, "sink"), C.byref(flop)))
+        return flop.value
+
     def append(self, cache: KvCache, k, v, token_count: int) -> None:
         cache.append_device(_dev(k, "k"), _dev(v, "v"), token_count)
 
