@@ -538,6 +538,10 @@ CONFIG_CASES = [
     ("gemma3_4b_chunk_128_on_16384_local_w1024", 4, 8, 8, 4, 256, 128, 16384, 1024, False),
     ("gemma3_4b_decode_16512_global", 4, 5, 8, 4, 256, 1, 16512, 0, False),
     ("gemma3_4b_decode_16512_local_w1024", 4, 8, 8, 4, 256, 1, 16512, 1024, False),
+    # one GPU's share of config 2 split 8 ways by KV head (one KV head and its
+    # three query heads per GPU): the kernels at that real shape
+    ("llama32_3b_decode_8192_tp8_share", 2, 28, 3, 1, 128, 1, 8192, 0, True),
+    ("llama32_3b_prefill_4096_tp8_share", 2, 28, 3, 1, 128, 4096, 0, 0, False),
 ]
 
 

@@ -32,4 +32,7 @@ def test_prefill_pairs_and_flop():
 
 
 def test_config_cases_cover_every_other_baseline_config():
-    assert {c[1] for c in bench.CONFIG_CASES} == {0, 1, 3, 4}  # config 2 is the main bench
+    # config 2 is the main bench; its cases here are one GPU's share of an 8-way head split
+    assert {c[1] for c in bench.CONFIG_CASES if "tp8_share" not in c[0]} == {0, 1, 3, 4}
+    shares = [c for c in bench.CONFIG_CASES if "tp8_share" in c[0]]
+    assert shares and all(c[1] == 2 and (c[3], c[4], c[5]) == (24 // 8, 8 // 8, 128) for c in shares)
