@@ -262,8 +262,8 @@ typedef enum {
 } spissa_kernel_path;
 typedef struct {
     int path;               /* spissa_kernel_path */
-    int heads_per_block;    /* decode: query heads sharing one K/V read */
-    int head_blocks;        /* decode: head blocks per KV head */
+    int heads_per_block;    /* query heads sharing one K/V read (decode) or one workgroup (prefill) */
+    int head_blocks;        /* head blocks per KV head */
     int keys_per_split;     /* decode: cached keys per split workgroup */
     int splits;             /* decode: splits of the longest sequence, the token's own included; prefill: key splits (1: none) */
     int token_split;        /* decode: the new token has a split of its own after the cached keys' (else split 0 takes it) */

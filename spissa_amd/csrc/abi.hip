@@ -1155,7 +1155,7 @@ static void plan_prefill(PrefillArgs &a, int D, int cus, PrefillPlan *p) {
   }
   a.xcd_group = prefill_use_xcd_group(a, D) ? 1 : 0;
   const int wgq = prefill_wg_queries(a, D);
-  p->workgroups = (size_t)prefill_grid_workgroups((S + wgq - 1) / wgq, a.R / (128 / wgq), a.Hkv, a.splits,
+  p->workgroups = (size_t)prefill_grid_workgroups((S + wgq - 1) / wgq, a.R / prefill_wg_heads(a, D), a.Hkv, a.splits,
                                                   a.xcd_group);
 }
 
@@ -1539,6 +1539,8 @@ extern "C" int spissa_plan_attention(const spissa_kv_attention_config *cfg, cons
     out->tiles_per_split = a.tps;
     out->tile_keys = prefill_tile_keys(D);
     out->workgroup_queries = prefill_wg_queries(a, D);
+    out->heads_per_block = prefill_wg_heads(a, D);
+    out->head_blocks = a.R / out->heads_per_block;
     out->o_split = a.o_split;
     out->xcd_group = a.xcd_group;
     out->max_tiles = p.tiles;

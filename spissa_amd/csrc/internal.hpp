@@ -135,6 +135,8 @@ struct PrefillArgs {
 int prefill_wgs_per_cu(int D);
 int prefill_tile_keys(int D);
 int prefill_wg_queries(const PrefillArgs &a, int D);
+int prefill_wg_heads(const PrefillArgs &a, int D);  // query heads per workgroup
+bool prefill_half_wg(const PrefillArgs &a, int D);   // half-size workgroups (windowed head_dim 256)
 // Workgroups one (unsplit) prefill launch would have.
 long prefill_base_workgroups(const PrefillArgs &a, int D);
 // Most key tiles one (unsplit) prefill workgroup visits.

@@ -717,9 +717,19 @@ hipError_t launch_shape(hipStream_t st, PrefillArgs a) {
 // wave halves the LDS fragment reads per
 // MFMA but, at head_dim 128, needs more than 256 VGPRs and measured slower;
 // at head_dim 64 it halves the workgroup count, which a 2048-token prefill
-// cannot afford.)
+// cannot afford.) Windowed head_dim-256 layers run half-size workgroups (two
+// heads, or one head with two blocks): their short key ranges leave CUs idle
+// with the full size (Gemma-3-1B's W512 layer 43.1 -> 40.5 us, Gemma-3-4B's
+// W1024 chunk 30.6 -> 27.7 us), while the long causal ranges of the global
+// layers run 30-40% slower with them.
 template <int D, int BN, int OS>
 hipError_t launch_r(hipStream_t st, const PrefillArgs &a) {
+  if constexpr (D >= 256) {
+    if (prefill_half_wg(a, D)) {
+      if (a.R % 2 == 0) return launch_shape<D, 2, 1, BN, 1, OS>(st, a);
+      return launch_shape<D, 1, 2, BN, 1, OS>(st, a);
+    }
+  }
   if (a.R % 4 == 0) return launch_shape<D, 4, 1, BN, 1, OS>(st, a);
   if (a.R % 2 == 0) return launch_shape<D, 2, 2, BN, 1, OS>(st, a);
   return launch_shape<D, 1, 4, BN, 1, OS>(st, a);
@@ -740,16 +750,23 @@ hipError_t launch_d(hipStream_t st, const PrefillArgs &a) {
 
 bool prefill_supported(int D) { return D == 64 || D == 128 || D == 256; }
 
-// Four-wave workgroups of 32 queries per wave: four heads x 32 queries, two
-// heads x 64, or one head x 128 (launch_d above).
-int prefill_wg_queries(const PrefillArgs &a, int) { return a.R % 4 == 0 ? 32 : a.R % 2 == 0 ? 64 : 128; }
+// Workgroups of 32 queries per wave (launch_r above): four heads x 32
+// queries, two heads x 64, or one head x 128; half-size ones two heads x 32
+// or one head x 64.
+bool prefill_half_wg(const PrefillArgs &a, int D) { return D >= 256 && a.window > 0; }
+int prefill_wg_heads(const PrefillArgs &a, int D) {
+  if (prefill_half_wg(a, D)) return a.R % 2 == 0 ? 2 : 1;
+  return a.R % 4 == 0 ? 4 : a.R % 2 == 0 ? 2 : 1;
+}
+int prefill_wg_queries(const PrefillArgs &a, int D) {
+  return (prefill_half_wg(a, D) ? 64 : 128) / prefill_wg_heads(a, D);
+}
 int prefill_wgs_per_cu(int D) { return D >= 256 ? 1 : 2; }
 int prefill_tile_keys(int D) { return D >= 256 ? 32 : 64; }  // BN of launch_d
 
 long prefill_base_workgroups(const PrefillArgs &a, int D) {
   const int wgq = prefill_wg_queries(a, D);
-  const int rb = 128 / wgq;
-  return (long)((a.S + wgq - 1) / wgq) * a.Hkv * (a.R / rb);
+  return (long)((a.S + wgq - 1) / wgq) * a.Hkv * (a.R / prefill_wg_heads(a, D));
 }
 
 long prefill_grid_workgroups(long n_qblocks, long head_blocks, long Hkv, long splits, int xcd_group) {
@@ -760,7 +777,7 @@ long prefill_grid_workgroups(long n_qblocks, long head_blocks, long Hkv, long sp
 
 bool prefill_use_xcd_group(const PrefillArgs &a, int D) {
   const int wgq = prefill_wg_queries(a, D);
-  const long G = (long)(a.R / (128 / wgq)) * ((a.S + wgq - 1) / wgq);
+  const long G = (long)(a.R / prefill_wg_heads(a, D)) * ((a.S + wgq - 1) / wgq);
   return a.splits > 1 && (long)a.Hkv * a.splits >= 8 && G > 1;
 }
 

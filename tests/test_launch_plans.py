@@ -124,8 +124,11 @@ def check_prefill(cfg, P, plan):
     assert TILE_ALIGN % BN == 0
     key_total = P + S
     n_qblocks = -(-S // WGQ)
-    rb = 128 // WGQ
-    check_prefill_grid(plan, n_qblocks, Hkv, Hq // Hkv // rb, splits)
+    rb = plan["heads_per_block"]
+    # 32 queries per wave, four waves per workgroup (two: windowed head_dim 256)
+    assert rb * WGQ == (64 if D >= 256 and W > 0 else 128)
+    assert plan["head_blocks"] * rb == Hq // Hkv
+    check_prefill_grid(plan, n_qblocks, Hkv, plan["head_blocks"], splits)
     P8 = P & ~(TILE_ALIGN - 1)
     cap_stage = ((P + S + TILE_ALIGN - 1) & ~(TILE_ALIGN - 1)) - P8
     assert plan["stage_bytes"] == 2 * Hkv * cap_stage * D * 2
