@@ -318,6 +318,10 @@ prefill_kernel(const PrefillArgs a) {
   const char *kb_s = reinterpret_cast<const char *>(a.kb_stage + (long)h * a.cap_stage * D);
   const char *vt_c = reinterpret_cast<const char *>(a.vt_cache + (long)h * D * a.cap_cache);
   const char *vt_s = reinterpret_cast<const char *>(a.vt_stage + (long)h * D * a.cap_stage);
+  // V^T row strides held in scalar registers (otherwise reloaded from the
+  // kernel arguments, with a wait, on every step)
+  const unsigned vt_stride_c = __builtin_amdgcn_readfirstlane((unsigned)a.cap_cache);
+  const unsigned vt_stride_s = __builtin_amdgcn_readfirstlane((unsigned)a.cap_stage);
 
   // Tiles below P8 come from the cache shadow, the others from staging (P8 is
   // a multiple of the tile width, so the choice is uniform per tile).
@@ -331,7 +335,7 @@ prefill_kernel(const PrefillArgs a) {
     const int nk = t * BN;
     const bool cached = nk < a.P8;
     const char *src = cached ? vt_c + (long)nk * 2 : vt_s + (long)(nk - a.P8) * 2;
-    const unsigned stride = (unsigned)(cached ? a.cap_cache : a.cap_stage);
+    const unsigned stride = cached ? vt_stride_c : vt_stride_s;
 #pragma unroll
     for (int j = 0; j < G::VDMA; ++j) dma16(src + v_src(j, stride), dst + (wave + j * NW) * 1024);
   };
