@@ -18,7 +18,7 @@
 //  - linear_gemm_kernel (bf16 weights, M > 64, K % 32 == 0: prefill): MFMA
 //    v_mfma_f32_32x32x16_bf16 on 128 x 128 output tiles, 32-deep k tiles in
 //    LDS (weights copied global -> LDS with global_load_lds_dwordx4,
-//    activations converted in registers). Each f32 activation is split into
+//    activations converted in registers), three workgroups per CU. Each f32 activation is split into
 //    bf16 hi = rne(x) and lo = rne(x - hi), and both halves meet the bf16
 //    weight: the products are exact in f32 and the residual of the split is
 //    below 2^-16 |x|, so the result carries f32-level error rather than bf16.
@@ -205,16 +205,19 @@ __device__ __forceinline__ unsigned bf16x2_rne(float a, float b) {
 // Grid: ceil(M / 128) * ceil(N / 128) workgroups of 256 threads (2 x 2 waves,
 // 64 x 64 outputs each). K % 32 == 0. Rows past M or N are read clamped and
 // not stored.
-// Pipeline, per 32-deep k tile t: the weight tile is copied into one of three
-// LDS buffers two steps ahead (issued in step t-2), and the activations are
+// Pipeline, per 32-deep k tile t: the weight tile is copied into one of two
+// LDS buffers one step ahead (issued in step t-1), and the activations are
 // loaded into registers two steps ahead (issued in step t-2, split and written
 // to one of two LDS buffers at the start of step t-1). Step t writes the
-// activations of tile t+1, issues the loads of tile t+2, runs the 16 MFMAs of
-// tile t per wave, then waits for everything but the loads it just issued.
-__global__ __launch_bounds__(256, 2) void linear_gemm_kernel(const LinearArgs a) {
+// activations of tile t+1, copies the weights of tile t+1, loads the
+// activations of tile t+2, runs the 16 MFMAs of tile t per wave, then waits
+// for everything but the activation loads it just issued. 48 KB of LDS and
+// at most 168 VGPRs let three workgroups share a CU (three waves per SIMD):
+// 292 us against 342 us for the 4096 x 5120 x 3072 projection with a third
+// weight buffer two steps ahead and two workgroups per CU.
+__global__ __launch_bounds__(256, 3) void linear_gemm_kernel(const LinearArgs a) {
   __shared__ __attribute__((aligned(1024))) char w_lds0[kBN * kRowBytes];
   __shared__ __attribute__((aligned(1024))) char w_lds1[kBN * kRowBytes];
-  __shared__ __attribute__((aligned(1024))) char w_lds2[kBN * kRowBytes];
   __shared__ __attribute__((aligned(1024))) char xh_lds0[kBM * kRowBytes];
   __shared__ __attribute__((aligned(1024))) char xh_lds1[kBM * kRowBytes];
   __shared__ __attribute__((aligned(1024))) char xl_lds0[kBM * kRowBytes];
@@ -317,57 +320,45 @@ __global__ __launch_bounds__(256, 2) void linear_gemm_kernel(const LinearArgs a)
     }
   };
 
-  // One step on tile t; W selects the weight buffers (t % 3 computes, (t+2) % 3
-  // receives), X the activation buffers (t % 2 computes, (t+1) % 2 receives),
-  // xnext holds tile t+1's activations and receives tile t+2's.
-  auto step = [&](auto W_, auto X_, int t, float4 (&xnext)[4]) {
-    constexpr int W = decltype(W_)::value, X = decltype(X_)::value;
-    char *const w_cur = W == 0 ? w_lds0 : W == 1 ? w_lds1 : w_lds2;
-    char *const w_fill = W == 0 ? w_lds2 : W == 1 ? w_lds0 : w_lds1;
-    char *const xh_cur = X ? xh_lds1 : xh_lds0, *const xl_cur = X ? xl_lds1 : xl_lds0;
-    char *const xh_fill = X ? xh_lds0 : xh_lds1, *const xl_fill = X ? xl_lds0 : xl_lds1;
-    if (t + 1 < nk) store_x(xnext, xh_fill, xl_fill);
-    const bool more = t + 2 < nk;
-    if (more) {
-      copy_w(t + 2, w_fill);
-      load_x(t + 2, xnext);
+  // One step on tile t; B selects the buffers (t % 2 computes, (t+1) % 2
+  // receives): the weights of tile t+1 are copied one step ahead, the
+  // activations loaded two ahead and written one ahead.
+  auto step = [&](auto B_, int t, float4 (&xnext)[4]) {
+    constexpr int B = decltype(B_)::value;
+    char *const w_cur = B ? w_lds1 : w_lds0, *const w_fill = B ? w_lds0 : w_lds1;
+    char *const xh_cur = B ? xh_lds1 : xh_lds0, *const xl_cur = B ? xl_lds1 : xl_lds0;
+    char *const xh_fill = B ? xh_lds0 : xh_lds1, *const xl_fill = B ? xl_lds0 : xl_lds1;
+    if (t + 1 < nk) {
+      store_x(xnext, xh_fill, xl_fill);
+      copy_w(t + 1, w_fill);
     }
+    const bool more = t + 2 < nk;
+    if (more) load_x(t + 2, xnext);
     compute(w_cur, xh_cur, xl_cur);
-    // all loads but this step's (2 weight copies + 4 activation loads) are done
-    if (more) __builtin_amdgcn_s_waitcnt(0x0F76);  // vmcnt(6)
+    // everything but this step's activation loads is done
+    if (more) __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4)
     else __builtin_amdgcn_s_waitcnt(0x0F70);       // vmcnt(0)
     __syncthreads();
   };
 
-  // Prologue: weights of tiles 0 and 1 copied, activations of tile 0 in LDS,
-  // tile 1's in registers.
+  // Prologue: weights of tile 0 copied, activations of tile 0 in LDS, tile
+  // 1's in registers.
   float4 xv[4];
   copy_w(0, w_lds0);
-  if (nk > 1) copy_w(1, w_lds1);
   load_x(0, xv);
   store_x(xv, xh_lds0, xl_lds0);
   if (nk > 1) load_x(1, xv);
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   __syncthreads();
 
-  // The buffer pattern repeats every 6 tiles.
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
-  using I2 = std::integral_constant<int, 2>;
   int t = 0;
-  for (; t + 6 <= nk; t += 6) {
-    step(I0(), I0(), t, xv);
-    step(I1(), I1(), t + 1, xv);
-    step(I2(), I0(), t + 2, xv);
-    step(I0(), I1(), t + 3, xv);
-    step(I1(), I0(), t + 4, xv);
-    step(I2(), I1(), t + 5, xv);
+  for (; t + 2 <= nk; t += 2) {
+    step(I0(), t, xv);
+    step(I1(), t + 1, xv);
   }
-  if (t < nk) step(I0(), I0(), t, xv);
-  if (t + 1 < nk) step(I1(), I1(), t + 1, xv);
-  if (t + 2 < nk) step(I2(), I0(), t + 2, xv);
-  if (t + 3 < nk) step(I0(), I1(), t + 3, xv);
-  if (t + 4 < nk) step(I1(), I0(), t + 4, xv);
+  if (t < nk) step(I0(), t, xv);
 
   // Accumulator layout: element e of lane l is row 8 (e / 4) + 4 hl + e % 4,
   // column lr of its 32 x 32 block.
