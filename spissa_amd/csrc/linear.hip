@@ -16,9 +16,9 @@
 //    decode): weight fragments straight from HBM into 16x16x32 MFMAs, the
 //    activations split as below, K split over the workgroup's four waves.
 //  - linear_gemm_kernel (bf16 weights, M > 64, K % 32 == 0: prefill): MFMA
-//    v_mfma_f32_32x32x16_bf16 on 128 x 128 output tiles, 32-deep k tiles in
+//    v_mfma_f32_32x32x16_bf16 on 128 x 256 output tiles, 32-deep k tiles in
 //    LDS (weights copied global -> LDS with global_load_lds_dwordx4,
-//    activations converted in registers), three workgroups per CU. Each f32 activation is split into
+//    activations converted in registers), four waves per SIMD. Each f32 activation is split into
 //    bf16 hi = rne(x) and lo = rne(x - hi), and both halves meet the bf16
 //    weight: the products are exact in f32 and the residual of the split is
 //    below 2^-16 |x|, so the result carries f32-level error rather than bf16.
@@ -186,7 +186,7 @@ __global__ __launch_bounds__(256) void linear_gemv_multi_kernel(const LinearSegm
 }
 
 namespace {
-constexpr int kBM = 128, kBN = 128, kBK = 32;  // GEMM tiles
+constexpr int kBM = 128, kBN = 256, kBK = 32;  // GEMM tiles
 constexpr int kRowBytes = kBK * 2;              // one bf16 tile row: 64 bytes, four 16-byte chunks
 
 // Chunk swizzle of a 64-byte LDS row: any 8 aligned consecutive rows reading
@@ -202,7 +202,7 @@ __device__ __forceinline__ unsigned bf16x2_rne(float a, float b) {
 }
 }  // namespace
 
-// Grid: ceil(M / 128) * ceil(N / 128) workgroups of 256 threads (2 x 2 waves,
+// Grid: ceil(M / 128) * ceil(N / 256) workgroups of 512 threads (2 x 4 waves,
 // 64 x 64 outputs each). K % 32 == 0. Rows past M or N are read clamped and
 // not stored.
 // Pipeline, per 32-deep k tile t: the weight tile is copied into one of two
@@ -211,11 +211,12 @@ __device__ __forceinline__ unsigned bf16x2_rne(float a, float b) {
 // to one of two LDS buffers at the start of step t-1). Step t writes the
 // activations of tile t+1, copies the weights of tile t+1, loads the
 // activations of tile t+2, runs the 16 MFMAs of tile t per wave, then waits
-// for everything but the activation loads it just issued. 48 KB of LDS and
-// at most 168 VGPRs let three workgroups share a CU (three waves per SIMD):
-// 292 us against 342 us for the 4096 x 5120 x 3072 projection with a third
-// weight buffer two steps ahead and two workgroups per CU.
-__global__ __launch_bounds__(256, 3) void linear_gemm_kernel(const LinearArgs a) {
+// for everything but the activation loads it just issued. 64 KB of LDS and
+// at most 128 VGPRs let two workgroups share a CU (four waves per SIMD).
+// Measured on the 4096 x 5120 x 3072 projection: 284 us; 128 x 128 tiles of
+// four waves took 292 us with this pipeline (three workgroups per CU) and
+// 342 us with a third weight buffer two steps ahead (two per CU).
+__global__ __launch_bounds__(512, 2) void linear_gemm_kernel(const LinearArgs a) {
   __shared__ __attribute__((aligned(1024))) char w_lds0[kBN * kRowBytes];
   __shared__ __attribute__((aligned(1024))) char w_lds1[kBN * kRowBytes];
   __shared__ __attribute__((aligned(1024))) char xh_lds0[kBM * kRowBytes];
@@ -228,11 +229,11 @@ __global__ __launch_bounds__(256, 3) void linear_gemm_kernel(const LinearArgs a)
   const int m0 = tm * kBM, n0 = tn * kBN;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const int wm = wave >> 1, wn = wave & 1;  // the wave's 64 x 64 quadrant
+  const int wm = wave >> 2, wn = wave & 3;  // the wave's 64 x 64 block
   const int lr = lane & 31, hl = lane >> 5;
   const int nk = a.K / kBK;
 
-  // Weight copies: 8 KB per tile = 8 copies of 1 KB, two per wave. Copy j of
+  // Weight copies: 16 KB per tile = 16 copies of 1 KB, two per wave. Copy j of
   // wave w fills LDS bytes [(2w + j) * 1024, +1024); lane l's 16 bytes land at
   // +16 l, i.e. row R = byte / 64, position p, which holds chunk p ^ swz4(R).
   const char *wg = reinterpret_cast<const char *>(a.w);
@@ -250,36 +251,32 @@ __global__ __launch_bounds__(256, 3) void linear_gemm_kernel(const LinearArgs a)
       __builtin_amdgcn_global_load_lds(wg + w_src[j] + (long)kt * kBK * 2, (lds_void *)(dst + (2 * wave + j) * 1024),
                                        16, 0, 0);
   };
-  // Activations: thread t loads row t / 2, columns 16 (t % 2) + [0, 16) of the
-  // k tile, splits them and writes 32 bytes of hi and of lo (chunks 2 (t % 2)
-  // and 2 (t % 2) + 1 of the row).
-  const int xr = tid >> 1, xc = tid & 1;
-  const float *xg = a.x + (long)min(m0 + xr, a.M - 1) * a.K + 16 * xc;
-  auto load_x = [&](int kt, float4 (&xv)[4]) {
+  // Activations: thread t loads row t / 4, columns 8 (t % 4) + [0, 8) of the
+  // k tile, splits them and writes 16 bytes of hi and of lo (chunk t % 4 of
+  // the row).
+  const int xr = tid >> 2, xc = tid & 3;
+  const float *xg = a.x + (long)min(m0 + xr, a.M - 1) * a.K + 8 * xc;
+  auto load_x = [&](int kt, float4 (&xv)[2]) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) xv[i] = *reinterpret_cast<const float4 *>(xg + (long)kt * kBK + 4 * i);
+    for (int i = 0; i < 2; ++i) xv[i] = *reinterpret_cast<const float4 *>(xg + (long)kt * kBK + 4 * i);
   };
-  auto store_x = [&](const float4 (&xv)[4], char *hi, char *lo) {
-    const float f[16] = {xv[0].x, xv[0].y, xv[0].z, xv[0].w, xv[1].x, xv[1].y, xv[1].z, xv[1].w,
-                         xv[2].x, xv[2].y, xv[2].z, xv[2].w, xv[3].x, xv[3].y, xv[3].z, xv[3].w};
-    unsigned h[8], l[8];
+  auto store_x = [&](const float4 (&xv)[2], char *hi, char *lo) {
+    const float f[8] = {xv[0].x, xv[0].y, xv[0].z, xv[0].w, xv[1].x, xv[1].y, xv[1].z, xv[1].w};
+    unsigned h[4], l[4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 4; ++i) {
       // one v_cvt_pk_bf16_f32 per pair (round to nearest even), for hi and for lo
       h[i] = bf16x2_rne(f[2 * i], f[2 * i + 1]);
       const float r0 = f[2 * i] - __uint_as_float(h[i] << 16);
       const float r1 = f[2 * i + 1] - __uint_as_float(h[i] & 0xffff0000u);
       l[i] = bf16x2_rne(r0, r1);
     }
-#pragma unroll
-    for (int cc = 0; cc < 2; ++cc) {
-      const int off = xr * kRowBytes + 16 * ((2 * xc + cc) ^ swz4(xr));
-      *reinterpret_cast<uint4 *>(hi + off) = make_uint4(h[4 * cc], h[4 * cc + 1], h[4 * cc + 2], h[4 * cc + 3]);
-      *reinterpret_cast<uint4 *>(lo + off) = make_uint4(l[4 * cc], l[4 * cc + 1], l[4 * cc + 2], l[4 * cc + 3]);
-    }
+    const int off = xr * kRowBytes + 16 * (xc ^ swz4(xr));
+    *reinterpret_cast<uint4 *>(hi + off) = make_uint4(h[0], h[1], h[2], h[3]);
+    *reinterpret_cast<uint4 *>(lo + off) = make_uint4(l[0], l[1], l[2], l[3]);
   };
 
-  // Fragment offsets: block b of the quadrant, 16-deep k step s: row
+  // Fragment offsets: block b of the wave's 64 x 64 block, 16-deep k step s: row
   // 32 b + lr, chunk 2 s + hl (32 b leaves swz4 unchanged).
   unsigned a_rd[2][2], b_rd[2][2];
 #pragma unroll
@@ -323,7 +320,7 @@ __global__ __launch_bounds__(256, 3) void linear_gemm_kernel(const LinearArgs a)
   // One step on tile t; B selects the buffers (t % 2 computes, (t+1) % 2
   // receives): the weights of tile t+1 are copied one step ahead, the
   // activations loaded two ahead and written one ahead.
-  auto step = [&](auto B_, int t, float4 (&xnext)[4]) {
+  auto step = [&](auto B_, int t, float4 (&xnext)[2]) {
     constexpr int B = decltype(B_)::value;
     char *const w_cur = B ? w_lds1 : w_lds0, *const w_fill = B ? w_lds0 : w_lds1;
     char *const xh_cur = B ? xh_lds1 : xh_lds0, *const xl_cur = B ? xl_lds1 : xl_lds0;
@@ -336,14 +333,14 @@ __global__ __launch_bounds__(256, 3) void linear_gemm_kernel(const LinearArgs a)
     if (more) load_x(t + 2, xnext);
     compute(w_cur, xh_cur, xl_cur);
     // everything but this step's activation loads is done
-    if (more) __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4)
+    if (more) __builtin_amdgcn_s_waitcnt(0x0F72);  // vmcnt(2)
     else __builtin_amdgcn_s_waitcnt(0x0F70);       // vmcnt(0)
     __syncthreads();
   };
 
   // Prologue: weights of tile 0 copied, activations of tile 0 in LDS, tile
   // 1's in registers.
-  float4 xv[4];
+  float4 xv[2];
   copy_w(0, w_lds0);
   load_x(0, xv);
   store_x(xv, xh_lds0, xl_lds0);
@@ -564,7 +561,7 @@ hipError_t launch_linear(hipStream_t st, const LinearArgs &a, int path) {
   if (path == kLinearGemm) {
     if (a.dtype != SPISSA_DTYPE_BF16 || a.K % kBK != 0) return hipErrorInvalidValue;
     const long grid = (long)((a.M + kBM - 1) / kBM) * ((a.N + kBN - 1) / kBN);
-    hipLaunchKernelGGL(linear_gemm_kernel, dim3((unsigned)grid), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(linear_gemm_kernel, dim3((unsigned)grid), dim3(512), 0, st, a);
     return hipGetLastError();
   }
   switch (a.dtype) {
