@@ -919,7 +919,10 @@ def configs_only(args) -> dict:
         sess.sync()
         return a.elapsed_time(b) / reps
 
-    return configs_bench(sess, stream, gen, dev, args, time_graph)
+    out = configs_bench(sess, stream, gen, dev, args, time_graph)
+    if "projections" in args.configs.split(","):
+        out["projections"] = projection_bench(sess, stream, gen, dev, args, time_graph)
+    return out
 
 
 def cpu_model() -> str:
@@ -1077,8 +1080,9 @@ def main() -> int:
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a 256 MiB device copy (HBM-counter calibration under rocprofv3 --pmc)")
     ap.add_argument("--configs", default="",
-                    help="only time these comma-separated cases of CONFIG_CASES and print their records "
-                         "(for counter passes); the benchmark line is not printed")
+                    help="only time these comma-separated cases of CONFIG_CASES (and 'projections': the "
+                         "q/k/v projection at batch 1, 16 and 4096) and print their records (for counter "
+                         "passes); the benchmark line is not printed")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build's attention path has no multi-GPU leg "
