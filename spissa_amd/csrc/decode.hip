@@ -405,18 +405,21 @@ __global__ __launch_bounds__(256, 4) void decode_split_kernel(const DecodeArgs a
 }
 
 // Finishes the attention of one (sequence, KV head, head block): merges the
-// partials of every split (the last one holds the new token) into O / L.
+// partials of every split (split 0 holds the new token) into O / L.
 // Grid: (Hkv*HB, RB*D / OUTS, B), the head blocks fastest as in the split
 // kernel: consecutive workgroups go to consecutive XCDs, so the combine of a
 // head runs on the XCD whose workgroups wrote that head's partials (measured
-// 4% faster per batch-1 layer at 8192 keys). 1024 threads = OUTS consecutive outputs x
-// SL split lanes (64 x 16, or 16 x 64 when there are many splits). Each lane
-// keeps an online (max, sum, output) over its splits with the loads of eight
-// splits in flight; the SL lanes of every output are merged through LDS.
-template <int D, int RB, int SL>
-__global__ __launch_bounds__(1024) void decode_combine_kernel(const DecodeArgs a) {
+// 4% faster per batch-1 layer at 8192 keys). NT threads = OUTS consecutive
+// outputs x SL split lanes: 16 x 16 in 256-thread workgroups, or 16 x 64 in
+// 1024-thread ones when there are many splits (256 threads for 16 lanes
+// measured 3-4% faster per batch-1 layer than 1024, and 64 or 128 threads
+// slower). Each lane keeps an online (max, sum, output) over its splits with
+// the loads of eight splits in flight; the SL lanes of every output are
+// merged through LDS.
+template <int D, int RB, int SL, int NT>
+__global__ __launch_bounds__(NT) void decode_combine_kernel(const DecodeArgs a) {
   constexpr int ENTRY = RB * (D + 2);
-  constexpr int OUTS = 1024 / SL, UNROLL = 8;  // one load round up to SL * 8 splits
+  constexpr int OUTS = NT / SL, UNROLL = 8;  // one load round up to SL * 8 splits
   __shared__ float s_m[SL][OUTS], s_l[SL][OUTS], s_o[SL][OUTS];
 
   const int hb = blockIdx.x % a.HB;
@@ -512,10 +515,10 @@ hipError_t launch_one(hipStream_t st, const DecodeArgs &a) {
   }
   if (a.max_splits > kCombineWideSplits) {
     dim3 cgrid((unsigned)(a.Hkv * a.HB), (unsigned)(RB * D / 16), (unsigned)a.B);
-    hipLaunchKernelGGL((decode_combine_kernel<D, RB, 64>), cgrid, dim3(1024), 0, st, a);
+    hipLaunchKernelGGL((decode_combine_kernel<D, RB, 64, 1024>), cgrid, dim3(1024), 0, st, a);
   } else {
-    dim3 cgrid((unsigned)(a.Hkv * a.HB), (unsigned)(RB * D / 64), (unsigned)a.B);
-    hipLaunchKernelGGL((decode_combine_kernel<D, RB, 16>), cgrid, dim3(1024), 0, st, a);
+    dim3 cgrid((unsigned)(a.Hkv * a.HB), (unsigned)(RB * D / 16), (unsigned)a.B);
+    hipLaunchKernelGGL((decode_combine_kernel<D, RB, 16, 256>), cgrid, dim3(256), 0, st, a);
   }
   return hipGetLastError();
 }
