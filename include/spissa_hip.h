@@ -270,7 +270,7 @@ typedef struct {
     int tiles_per_split;    /* prefill with key splits: key tiles per split */
     int tile_keys;          /* prefill: keys per tile */
     int workgroup_queries;  /* prefill: queries per workgroup */
-    int o_split;            /* prefill: head_dim-256 output split over two waves */
+    int o_split;            /* always 0 (no kernel splits O over waves; kept for the struct's layout) */
     int xcd_group;          /* prefill with key splits: the workgroups of one KV head's split share an XCD */
     long max_tiles;         /* prefill: most key tiles one unsplit workgroup visits */
     size_t workgroups;      /* attention kernel grid (decode: its first launch of <= 16 sequences) */

@@ -1141,17 +1141,13 @@ static void plan_prefill(PrefillArgs &a, int D, int cus, PrefillPlan *p) {
       p->ppart_bytes = (size_t)a.splits * S * a.Hq * (D + 2) * sizeof(float);
     }
   }
-  // head_dim 256: the O split (two waves per (head, query block), each with
-  // half the score and output MFMAs) where a workgroup covers at least 8 key
-  // tiles. Windowed layers with at least one workgroup per two CUs run it
+  // Windowed head_dim-256 layers with at least one workgroup per two CUs run
   // unsplit: the key-split combine costs more than the CUs left idle
   // (measured on Gemma-3-1B's W512 layer: 42.8 against 46.6 us).
-  a.o_split = D >= 256 && (a.splits > 1 ? a.tps : p->tiles) >= 8;
   if (D >= 256 && a.window > 0 && base * 2 >= cus) {
     a.splits = 1;
     a.tps = 0;
     p->ppart_bytes = 0;
-    a.o_split = 1;
   }
   a.xcd_group = prefill_use_xcd_group(a, D) ? 1 : 0;
   const int wgq = prefill_wg_queries(a, D);
@@ -1541,7 +1537,7 @@ extern "C" int spissa_plan_attention(const spissa_kv_attention_config *cfg, cons
     out->workgroup_queries = prefill_wg_queries(a, D);
     out->heads_per_block = prefill_wg_heads(a, D);
     out->head_blocks = a.R / out->heads_per_block;
-    out->o_split = a.o_split;
+    out->o_split = 0;
     out->xcd_group = a.xcd_group;
     out->max_tiles = p.tiles;
     out->workgroups = p.workgroups;

@@ -119,10 +119,6 @@ struct PrefillArgs {
   // key); launch_prefill_combine merges them. splits == 1 writes `out`.
   int splits, tps;
   float *part_o, *part_ml;
-  // head_dim 256: split O over two waves per (head, query block). It costs
-  // 1.5x the MFMAs (both waves compute the scores) and doubles the waves per
-  // SIMD, which pays off on long key ranges per workgroup.
-  int o_split;
   // With key splits: the workgroups that read one KV head's split (its head
   // blocks and query blocks) are given ids 8 apart, so they run on one XCD
   // and share its L2 (prefill_use_xcd_group decides; the grid is padded to a
@@ -136,7 +132,6 @@ int prefill_wgs_per_cu(int D);
 int prefill_tile_keys(int D);
 int prefill_wg_queries(const PrefillArgs &a, int D);
 int prefill_wg_heads(const PrefillArgs &a, int D);  // query heads per workgroup
-bool prefill_half_wg(const PrefillArgs &a, int D);   // half-size workgroups (windowed head_dim 256)
 // Workgroups one (unsplit) prefill launch would have.
 long prefill_base_workgroups(const PrefillArgs &a, int D);
 // Most key tiles one (unsplit) prefill workgroup visits.

@@ -6,11 +6,12 @@
 // tiles below P8, the staging buffer for the rest); scores, softmax state and
 // the output accumulate in f32.
 //
-// Work split. Each wave owns QB 32-query blocks of one query head (QB = 1 in
-// the launched configurations), and the four waves of a workgroup share one KV
-// head: four heads of a group, two heads with two blocks each, or one head
-// with four blocks. Two waves run per SIMD (at most 256 VGPRs each) up to
-// head_dim 128; head_dim 256 runs one wave per SIMD with 32-key tiles.
+// Work split. At head_dim 64 and 128 (prefill_kernel) each wave owns QB
+// 32-query blocks of one query head (QB = 1 in the launched configurations),
+// and the four waves of a workgroup share one KV head: four heads of a group,
+// two heads with two blocks each, or one head with four blocks; two waves run
+// per SIMD (at most 256 VGPRs each). Head_dim 256 (prefill_q16_kernel, after
+// prefill_kernel) gives each wave 16 queries on 16x16x32 MFMAs, 32-key tiles.
 // Key splits (PrefillArgs::splits > 1) add workgroups over the key range for
 // grids too small to fill the GPU (short chunks over long caches, few heads);
 // prefill_combine_kernel merges their partial results.
@@ -30,9 +31,9 @@
 // are in flight while
 //   part A: the exponentials of tile t run on the VALU next to the MFMAs of
 //           S(t+1) = K(t+1) Q^T;
-//   part B: O^T += V(t)^T P(t)^T runs on the MFMAs (at head_dim 64 and 256
-//           next to the row maxima of tile t+1, which fix the exponent
-//           reference of step t+1);
+//   part B: O^T += V(t)^T P(t)^T runs on the MFMAs (at head_dim 64 next to
+//           the row maxima of tile t+1, which fix the exponent reference of
+//           step t+1);
 // then the (rare) rescale of O and one barrier. The compiler interleaves the
 // VALU and MFMA work of each part freely.
 // Scores. Q is rounded to bf16 after scaling by softmax scale * log2(e), and
@@ -47,8 +48,8 @@
 //   K tile   [BN keys][D]: chunk c of key row r at byte r*2D  + 16*(c ^ swz(r))
 //   V^T tile [D][BN keys]: chunk c of dim row d at byte d*2BN + 16*(c ^ swz(d))
 // Softmax. The exponent reference m of a row is raised rarely: at head_dim
-// 64 and 256 when the next tile's row maximum exceeds it by more than 8
-// (log2 domain); at head_dim 128 only when a tile's probabilities sum past
+// 64 when the next tile's row maximum exceeds it by more than 8 (log2
+// domain); at head_dim 128 and 256 only when a tile's probabilities sum past
 // 2^16 (or the row has seen no key yet), which drops the per-tile row
 // maximum. O and the sum share m, so O / sum is exact softmax arithmetic.
 // Row sums add the bf16 probabilities that the PV MFMAs use.
@@ -69,10 +70,10 @@ typedef __attribute__((ext_vector_type(16))) float f32x16;
 typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr float NEG_INF = -__builtin_inff();
-// Eager raising (head_dim 64 and 256): the largest growth of a row maximum
+// Eager raising (head_dim 64): the largest growth of a row maximum
 // (log2 domain) absorbed without rescaling, checked on every tile.
 constexpr float kRescaleSlack = 8.0f;
-// Lazy raising (head_dim 128): a lane's sum of one tile's probabilities above
+// Lazy raising (head_dim 128 and 256): a lane's sum of one tile's probabilities above
 // which its row's exponent reference is raised (the probabilities then stay
 // far from f32 and bf16 overflow, and O keeps full relative precision).
 constexpr float kRaiseSum = 65536.0f;
@@ -162,29 +163,21 @@ __device__ __forceinline__ float sum_bf16x8(const bf16x8 p) {
 
 }  // namespace
 
-// QB query blocks of 32 per wave (1 or 2); two waves per SIMD unless the
-// accumulators need the whole register file (two 128-wide blocks).
-// OS: waves sharing one (head, query block), each holding D / OS columns of
-// Q and O. With OS = 2 each wave computes the partial scores of its half of
-// the head dims; the two partials are exchanged through LDS and added in a
-// fixed order (the half with the exponent bias first), so both waves hold
-// the same score tile and the same softmax state, and each accumulates its
-// half of O^T += V^T P^T. Half the O and Q registers lets two waves share a
-// SIMD at head_dim 256, with no MFMA done twice.
-template <int D, int RB, int NPB, int BN, int QB, int OS>
-__global__ __launch_bounds__(RB *NPB *OS * 64, (OS == 1 && ((QB == 1 && D <= 128) || D <= 64)) ? 2 : 1) void
-prefill_kernel(const PrefillArgs a) {
-  constexpr int NW = RB * NPB * OS;
+// Head_dim 64 and 128. QB query blocks of 32 per wave (1 in the launched
+// shapes); two waves per SIMD (the second __launch_bounds__ argument is the
+// minimum waves per SIMD: at most 256 VGPRs each).
+template <int D, int RB, int NPB, int BN, int QB>
+__global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillArgs a) {
+  static_assert(D <= 128, "head_dim 256 runs prefill_q16_kernel");
+  constexpr int NW = RB * NPB;
   constexpr int WQ = QB * 32;  // queries per wave
   constexpr int WGQ = NPB * WQ;
   using G = Geom<D, BN, NW>;
   // Exponent reference raised lazily (from the tile's probability sums) or
   // eagerly (from every next tile's row maxima): lazily measured 2-3% faster
-  // at head_dim 128, eagerly 4-5% faster at 64 and 256.
+  // at head_dim 128, eagerly 4-5% faster at 64.
   constexpr bool LAZY = D == 128;
-  constexpr int DT = G::DT, KB = G::KB, KS = G::KS, DB = G::DB / OS;  // DB: output blocks of this wave
-  constexpr int DTW = DT / OS;  // 16-dim score steps of this wave
-  static_assert(OS == 1 || (OS == 2 && !LAZY), "the score exchange runs with the eager reference");
+  constexpr int DT = G::DT, KB = G::KB, KS = G::KS, DB = G::DB;
 
   // Four separate LDS objects (not one array): the compiler then knows that
   // copies into one buffer do not alias reads of another and does not wait
@@ -193,8 +186,6 @@ prefill_kernel(const PrefillArgs a) {
   __shared__ __attribute__((aligned(1024))) char k_lds1[G::KBYTES];
   __shared__ __attribute__((aligned(1024))) char v_lds0[G::VBYTES];
   __shared__ __attribute__((aligned(1024))) char v_lds1[G::VBYTES];
-  // OS = 2: partial score tiles, two slots per wave (a 4-KB placeholder otherwise)
-  __shared__ __attribute__((aligned(16))) float s_x[2][OS == 2 ? NW : 1][OS == 2 ? QB * KB * 4 : 1][64][4];
 
   const int HB = a.R / RB;
   int h, hb, split, qt;
@@ -224,9 +215,7 @@ prefill_kernel(const PrefillArgs a) {
   // The wave index is uniform: readfirstlane keeps it (and all that derives
   // from it) in scalar registers and wave-level branches uniform.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int oh = wave / (RB * NPB);  // which D / OS columns of O this wave holds
-  const int r = wave % RB, pb = (wave / RB) % NPB;
-  const int d_base = oh * DB;
+  const int r = wave % RB, pb = wave / RB;
   const int head = h * a.R + hb * RB + r;
   const int p0 = qt * WGQ;
   const int wp0 = p0 + pb * WQ;
@@ -245,7 +234,7 @@ prefill_kernel(const PrefillArgs a) {
   }
   if (t_begin >= t_end) {  // this split sees none of the workgroup's keys (uniform exit)
     const int pos = wp0 + lane;
-    if (lane < WQ && pos < a.S && oh == 0) {
+    if (lane < WQ && pos < a.S) {
       float *ml = a.part_ml + (((long)split * a.S + pos) * a.Hq + head) * 2;
       ml[0] = -__builtin_inff();
       ml[1] = 0.0f;
@@ -257,19 +246,19 @@ prefill_kernel(const PrefillArgs a) {
   // Q carries the softmax scale times log2(e), so the scores come out of the
   // MFMAs in the log2 domain.
   const float c = a.qk_scale_log2;
-  bf16x8 qf[QB][DTW];
+  bf16x8 qf[QB][DT];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     const int pos = min(wp0 + 32 * qb + lq, a.S - 1);
     if (a.qb) {  // already scaled and rounded (the fused prefill step)
-      const bf16 *qp = a.qb + ((long)pos * a.Hq + head) * D + oh * (D / OS) + 8 * hl;
+      const bf16 *qp = a.qb + ((long)pos * a.Hq + head) * D + 8 * hl;
 #pragma unroll
-      for (int t = 0; t < DTW; ++t) qf[qb][t] = *reinterpret_cast<const bf16x8 *>(qp + 16 * t);
+      for (int t = 0; t < DT; ++t) qf[qb][t] = *reinterpret_cast<const bf16x8 *>(qp + 16 * t);
       continue;
     }
-    const float *qp = a.q + ((long)pos * a.Hq + head) * D + oh * (D / OS) + 8 * hl;
+    const float *qp = a.q + ((long)pos * a.Hq + head) * D + 8 * hl;
 #pragma unroll
-    for (int t = 0; t < DTW; ++t) {
+    for (int t = 0; t < DT; ++t) {
       const float4 x0 = *reinterpret_cast<const float4 *>(qp + 16 * t);
       const float4 x1 = *reinterpret_cast<const float4 *>(qp + 16 * t + 4);
       bf16x8 v;
@@ -292,9 +281,9 @@ prefill_kernel(const PrefillArgs a) {
 
   // LDS byte offsets of this lane's fragments (key block 0 / dim block 0).
   // (Rows of a fragment are 32 * block + lq, and 32 * block leaves swz unchanged.)
-  unsigned k_rd[DTW], v_rd[KS];
+  unsigned k_rd[DT], v_rd[KS];
 #pragma unroll
-  for (int t = 0; t < DTW; ++t) k_rd[t] = lq * 2 * D + 16 * ((2 * (oh * DTW + t) + hl) ^ swz<G::KNC>(lq));
+  for (int t = 0; t < DT; ++t) k_rd[t] = lq * 2 * D + 16 * ((2 * t + hl) ^ swz<G::KNC>(lq));
 #pragma unroll
   for (int t = 0; t < KS; ++t) v_rd[t] = lq * 2 * BN + 16 * ((2 * t + hl) ^ swz<G::VNC>(lq));
 
@@ -383,8 +372,7 @@ prefill_kernel(const PrefillArgs a) {
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             const int kk = kb * 32 + 8 * (i >> 2) + (i & 3);
-            // (with OS = 2 the mask and the bias go into the first half's partial)
-            s[qb][kb][i] = oh != 0 ? 0.0f : (kk < lo || kk > hi) ? NEG_INF : -ms[qb];
+            s[qb][kb][i] = (kk < lo || kk > hi) ? NEG_INF : -ms[qb];
           }
       }
       score_tile<D, BN, QB, 0, 1, false>(s, kbuf, k_rd, qf, bias);
@@ -405,38 +393,6 @@ prefill_kernel(const PrefillArgs a) {
     }
   };
 
-  // OS = 2: the partial score tile of tile t goes to LDS slot t & 1 (a lane's
-  // 16 scores of block (qb, kb) as four float4 rows of 64 lanes, conflict-free);
-  // after the next barrier the partner wave adds it to its own partial, the
-  // first half's partial (which holds the bias and the mask) first.
-  auto put_scores = [&](const f32x16 (&s)[QB][KB], int t) {
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-          *reinterpret_cast<float4 *>(&s_x[t & 1][wave][(qb * KB + kb) * 4 + g][lane][0]) =
-              make_float4(s[qb][kb][4 * g], s[qb][kb][4 * g + 1], s[qb][kb][4 * g + 2], s[qb][kb][4 * g + 3]);
-  };
-  auto add_partner_scores = [&](f32x16 (&s)[QB][KB], int t) {
-    const int partner = (wave + RB * NPB) % NW;
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const float4 p = *reinterpret_cast<const float4 *>(&s_x[t & 1][partner][(qb * KB + kb) * 4 + g][lane][0]);
-          const float pv[4] = {p.x, p.y, p.z, p.w};
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float own = s[qb][kb][4 * g + i];
-            s[qb][kb][4 * g + i] = oh == 0 ? own + pv[i] : pv[i] + own;
-          }
-        }
-  };
-
   // One pipelined step on tile t (scores in `cur`, exponent reference ms
   // already covering tile t, O and l already scaled to it):
   //   copies of K(t+2) and V(t+1) go out;
@@ -449,40 +405,6 @@ prefill_kernel(const PrefillArgs a) {
   // O selects the buffers.
   auto step = [&](auto O_, int t, f32x16 (&cur)[QB][KB], f32x16 (&nxt)[QB][KB]) {
     constexpr int O = decltype(O_)::value;
-    if constexpr (OS == 2) {
-      // The whole score tile t (the partner's half arrived at the last
-      // barrier), then the eager reference check on it, before its
-      // exponentials and before the bias of S(t+1) is used.
-      if (t != t_begin) {
-        add_partner_scores(cur, t);
-        float mx[QB];
-        row_max(cur, mx);
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-          const bool raise = mx[qb] > m[qb] + kRescaleSlack;
-          if (__ballot(raise)) {
-            const float mnew = raise ? mx[qb] : m[qb];
-            const float msn = mnew == NEG_INF ? 0.0f : mnew;
-            const float alpha = fast_exp2(m[qb] - msn), shift = msn - ms[qb];
-            l[qb] *= alpha;
-#pragma unroll
-            for (int d = 0; d < DB; ++d)
-#pragma unroll
-              for (int i = 0; i < 16; ++i) oacc[qb][d][i] *= alpha;
-#pragma unroll
-            for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-              for (int i = 0; i < 16; ++i) cur[qb][kb][i] -= shift;
-            m[qb] = mnew;
-            ms[qb] = msn;
-            if (oh == 0) {
-#pragma unroll
-              for (int i = 0; i < 16; ++i) bias[qb][i] = -ms[qb];
-            }
-          }
-        }
-      }
-    }
     char *const k_this = O ? k_lds1 : k_lds0;  // receives K(t+2)
     char *const k_next = O ? k_lds0 : k_lds1;  // holds K(t+1)
     char *const v_this = O ? v_lds1 : v_lds0;  // holds V(t)
@@ -508,8 +430,7 @@ prefill_kernel(const PrefillArgs a) {
         pf[qb][ks] = p;
       }
     }
-    score_tile<D, BN, QB, 1, DTW, false>(nxt, k_next, k_rd, qf, bias);
-    if constexpr (OS == 2) put_scores(nxt, t + 1);
+    score_tile<D, BN, QB, 1, DT, false>(nxt, k_next, k_rd, qf, bias);
 
     if constexpr (LAZY) {
     // The exponent reference is raised lazily: only a row whose probabilities
@@ -530,7 +451,9 @@ prefill_kernel(const PrefillArgs a) {
         const float mnew = mx > m[qb] ? mx : m[qb];
         const float msn = mnew == NEG_INF ? 0.0f : mnew;
         const float shift = msn - ms[qb];
-        const float alpha = fast_exp2(-shift);
+        // (from m, not ms: a row that has seen no key has m = -inf, ms = 0,
+        // nothing accumulated, and must scale by 0, not 2^-shift)
+        const float alpha = fast_exp2(m[qb] - msn);
         l[qb] *= alpha;
 #pragma unroll
         for (int d = 0; d < DB; ++d)
@@ -568,12 +491,12 @@ prefill_kernel(const PrefillArgs a) {
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
       for (int d = 0; d < DB; ++d) {
-        const bf16x8 vf = *reinterpret_cast<const bf16x8 *>(v_this + (d_base + d) * 64 * BN + v_rd[ks]);
+        const bf16x8 vf = *reinterpret_cast<const bf16x8 *>(v_this + d * 64 * BN + v_rd[ks]);
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb)
           oacc[qb][d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[qb][ks], oacc[qb][d], 0, 0, 0);
       }
-    if constexpr (!LAZY && OS == 1) {
+    if constexpr (!LAZY) {
     const bool has_next = t + 1 < t_end;
     float mx[QB], alpha[QB], shift[QB];
     bool raise[QB];
@@ -626,12 +549,7 @@ prefill_kernel(const PrefillArgs a) {
     for (int i = 0; i < 16; ++i) bias[qb][i] = 0.0f;
   }
   score_first(sa, k_lds0, t_begin);
-  score_tile<D, BN, QB, 1, DTW, false>(sa, k_lds0, k_rd, qf, bias);
-  if constexpr (OS == 2) {
-    put_scores(sa, t_begin);
-    __syncthreads();
-    add_partner_scores(sa, t_begin);
-  }
+  score_tile<D, BN, QB, 1, DT, false>(sa, k_lds0, k_rd, qf, bias);
   {
     float mx[QB];
     row_max(sa, mx);
@@ -643,10 +561,8 @@ prefill_kernel(const PrefillArgs a) {
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) sa[qb][kb][i] -= ms[qb];
-      if (oh == 0) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) bias[qb][i] = -ms[qb];
-      }
+      for (int i = 0; i < 16; ++i) bias[qb][i] = -ms[qb];
     }
   }
   __syncthreads();  // every wave is done with K(t0) before K(t0+2) lands in its buffer
@@ -663,14 +579,14 @@ prefill_kernel(const PrefillArgs a) {
       const float lt = xor32_sum(l[qb]);
       if (pos < a.S) {
         const long row = ((long)split * a.S + pos) * a.Hq + head;
-        float *op = a.part_o + row * D + 32 * d_base + 4 * hl;
+        float *op = a.part_o + row * D + 4 * hl;
 #pragma unroll
         for (int d = 0; d < DB; ++d)
 #pragma unroll
           for (int g = 0; g < 4; ++g)
             *reinterpret_cast<float4 *>(op + d * 32 + 8 * g) =
                 make_float4(oacc[qb][d][4 * g], oacc[qb][d][4 * g + 1], oacc[qb][d][4 * g + 2], oacc[qb][d][4 * g + 3]);
-        if (hl == 0 && oh == 0) {
+        if (hl == 0) {
           a.part_ml[row * 2] = m[qb];
           a.part_ml[row * 2 + 1] = lt;
         }
@@ -686,10 +602,10 @@ prefill_kernel(const PrefillArgs a) {
     const float lt = xor32_sum(l[qb]);
     if (pos < a.S) {
       // positive, finite and non-zero, tested on the bits (NaN fails it)
-      if (hl == 0 && oh == 0 && !(__float_as_uint(lt) - 1u < 0x7f7fffffu))
+      if (hl == 0 && !(__float_as_uint(lt) - 1u < 0x7f7fffffu))
         atomicOr(a.err, kDevErrSoftmaxDenominator);
       const float inv = 1.0f / lt;
-      float *op = a.out + ((long)pos * a.Hq + head) * D + 32 * d_base + 4 * hl;
+      float *op = a.out + ((long)pos * a.Hq + head) * D + 4 * hl;
 #pragma unroll
       for (int d = 0; d < DB; ++d)
 #pragma unroll
@@ -702,51 +618,385 @@ prefill_kernel(const PrefillArgs a) {
   }
 }
 
+
+// ---- 16-query waves (v_mfma_f32_16x16x32_bf16) ----
+namespace {
+typedef __attribute__((ext_vector_type(4))) float f32x4q;
+
+// Swizzle of the K tile rows read by 16-query waves: one score block reads key
+// rows {0..7, 16..23} (+8, +32 j) of the tile, and the 16 lanes one LDS read
+// serves take one chunk index of each: bits 0-2 and 4 of the row give 16
+// distinct chunks (8 distinct among any 8 aligned lanes).
+__device__ __forceinline__ constexpr int swz_k16(int row) { return (row & 7) | ((row >> 1) & 8); }
+
+// Key (within the tile) of row rho of 16-key score block b. Blocks 2j and 2j+1
+// cover keys [32j, 32j+32) so that lane group g (lanes 16g..16g+15) holds in
+// its four elements of block 2j, then of block 2j+1, the eight keys of V^T
+// slots 32j + 8g + [0, 8) in vt_key_slot order: P^T feeds the B operand of the
+// PV MFMA with no shuffle.
+__device__ __forceinline__ constexpr int key16(int b, int rho) {
+  return 32 * (b >> 1) + (rho < 8 ? rho : rho + 8) + 8 * (b & 1);
+}
+
+__device__ __forceinline__ float xor16_max(float v) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor16_sum(float v) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+}  // namespace
+
+// The head_dim-256 prefill: waves of 16 queries on v_mfma_f32_16x16x32_bf16.
+// A wave holds the whole head dim of its 16 queries (O^T 64 VGPRs, Q^T 32), so
+// no O split or score exchange between waves is needed and two four-wave
+// workgroups share a CU. RB heads x NPB blocks of 16 queries per workgroup,
+// BN-key tiles, the same copies, masks, pipeline and key splits as
+// prefill_kernel, lazy exponent reference.
+//   S^T = K Q^T   A = 16 key rows x 32 dims from LDS (rows key16(b, lane %
+//                 16)), B = Q^T in registers; lane l holds keys key16(b,
+//                 4 (l / 16) + i) of query l % 16;
+//   O^T += V^T P^T  A = 16 dim rows x 32 V^T slots from LDS, B = P^T from
+//                 the score registers (key16 makes them the slots' keys).
+template <int D, int RB, int NPB, int BN>
+__global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_q16_kernel(const PrefillArgs a) {
+  constexpr int NW = RB * NPB;
+  constexpr int WGQ = NPB * 16;
+  using G = Geom<D, BN, NW>;
+  constexpr int DT = D / 32;   // 32-dim steps of S^T = K Q^T
+  constexpr int KB = BN / 16;  // 16-key score blocks
+  constexpr int KS = BN / 32;  // 32-key steps of O^T += V^T P^T
+  constexpr int DB = D / 16;   // 16-dim output blocks
+  static_assert(D >= 128 && D / 8 >= 16, "swz_k16 needs 16 chunks per K row");
+
+  __shared__ __attribute__((aligned(1024))) char k_lds0[G::KBYTES];
+  __shared__ __attribute__((aligned(1024))) char k_lds1[G::KBYTES];
+  __shared__ __attribute__((aligned(1024))) char v_lds0[G::VBYTES];
+  __shared__ __attribute__((aligned(1024))) char v_lds1[G::VBYTES];
+
+  const int HB = a.R / RB;
+  int h, hb, split, qt;
+  if (a.xcd_group) {
+    const int Gq = HB * a.n_qblocks;
+    const int lo = (int)(blockIdx.x & 7), rest = (int)(blockIdx.x >> 3);
+    const int gg = rest % Gq, unit = (rest / Gq) * 8 + lo;
+    if (unit >= a.Hkv * a.splits) return;
+    h = unit % a.Hkv;
+    split = unit / a.Hkv;
+    hb = gg % HB;
+    qt = a.n_qblocks - 1 - gg / HB;
+  } else {
+    int bid = blockIdx.x;
+    const int hh = bid % (a.Hkv * HB);
+    bid /= (a.Hkv * HB);
+    split = bid % a.splits;
+    bid /= a.splits;
+    qt = a.n_qblocks - 1 - bid;
+    h = hh / HB;
+    hb = hh % HB;
+  }
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int r = wave % RB, pb = wave / RB;
+  const int head = h * a.R + hb * RB + r;
+  const int p0 = qt * WGQ;
+  const int wp0 = p0 + pb * 16;
+  const int lq = lane & 15, g = lane >> 4;
+  const int key_total = a.P + a.S;
+
+  int key_end = key_total;
+  if (a.causal) key_end = min(key_total, a.P + min(a.S, p0 + WGQ));
+  int key_begin = 0;
+  if (a.window > 0) key_begin = max(0, a.P + p0 - a.window + 1);
+  int t_begin = key_begin / BN;
+  int t_end = (key_end + BN - 1) / BN;
+  if (a.splits > 1) {
+    t_begin += split * a.tps;
+    t_end = min(t_end, t_begin + a.tps);
+  }
+  if (t_begin >= t_end) {
+    const int pos = wp0 + lane;
+    if (lane < 16 && pos < a.S) {
+      float *ml = a.part_ml + (((long)split * a.S + pos) * a.Hq + head) * 2;
+      ml[0] = -__builtin_inff();
+      ml[1] = 0.0f;
+    }
+    return;
+  }
+
+  // Q^T (B operand): lane holds query lq, dims 32t + 8g + [0, 8), carrying the
+  // softmax scale times log2(e).
+  bf16x8 qf[DT];
+  {
+    const int pos = min(wp0 + lq, a.S - 1);
+    if (a.qb) {
+      const bf16 *qp = a.qb + ((long)pos * a.Hq + head) * D + 8 * g;
+#pragma unroll
+      for (int t = 0; t < DT; ++t) qf[t] = *reinterpret_cast<const bf16x8 *>(qp + 32 * t);
+    } else {
+      const float c = a.qk_scale_log2;
+      const float *qp = a.q + ((long)pos * a.Hq + head) * D + 8 * g;
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+        const float4 x0 = *reinterpret_cast<const float4 *>(qp + 32 * t);
+        const float4 x1 = *reinterpret_cast<const float4 *>(qp + 32 * t + 4);
+        bf16x8 v;
+        v[0] = (bf16)(x0.x * c); v[1] = (bf16)(x0.y * c); v[2] = (bf16)(x0.z * c); v[3] = (bf16)(x0.w * c);
+        v[4] = (bf16)(x1.x * c); v[5] = (bf16)(x1.y * c); v[6] = (bf16)(x1.z * c); v[7] = (bf16)(x1.w * c);
+        qf[t] = v;
+      }
+    }
+  }
+  f32x4q o[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d) o[d] = f32x4q{0.0f, 0.0f, 0.0f, 0.0f};
+  float m = NEG_INF, l = 0.0f, ms = 0.0f;
+  f32x4q bias = f32x4q{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // LDS read offsets. K block b, dim step t: row key16(b, lq), chunk
+  // (4t + g) ^ swz_k16(row) = offset kbase[b] ^ (t << 6).
+  unsigned kbase[KB];
+#pragma unroll
+  for (int b = 0; b < KB; ++b) {
+    const int row = key16(b, lq), sw = swz_k16(row);
+    kbase[b] = (unsigned)(row * 2 * D + 16 * (g ^ (sw & 3)) + 64 * (sw >> 2));
+  }
+  // V^T dim block db, 32-key step s: row 16 db + lq, chunk (4s + g) ^ swz(row)
+  // (swz of the V^T tile depends on the row's low four bits only).
+  unsigned vbase;
+  {
+    const int sv = swz<G::VNC>(lq);
+    vbase = (unsigned)(lq * 2 * BN + 16 * (g ^ (sv & 3)) + 64 * (sv >> 2));
+  }
+
+  // Copies: copy j of the wave fills LDS bytes [(wave + j*NW) * 1024, +1024).
+  auto k_src = [&](int j) {
+    const int byte = (wave + j * NW) * 1024 + lane * 16;
+    const int row = byte / (2 * D), p = (byte % (2 * D)) / 16;
+    return (unsigned)(row * D + 8 * (p ^ swz_k16(row))) * 2u;
+  };
+  auto v_src = [&](int j, unsigned stride) {
+    const int byte = (wave + j * NW) * 1024 + lane * 16;
+    const int d = byte / (2 * BN), p = (byte % (2 * BN)) / 16;
+    return ((unsigned)d * stride + (unsigned)(8 * (p ^ swz<G::VNC>(d)))) * 2u;
+  };
+  const char *kb_c = reinterpret_cast<const char *>(a.kb_cache + (long)h * a.cap_cache * D);
+  const char *kb_s = reinterpret_cast<const char *>(a.kb_stage + (long)h * a.cap_stage * D);
+  const char *vt_c = reinterpret_cast<const char *>(a.vt_cache + (long)h * D * a.cap_cache);
+  const char *vt_s = reinterpret_cast<const char *>(a.vt_stage + (long)h * D * a.cap_stage);
+  const unsigned vt_stride_c = __builtin_amdgcn_readfirstlane((unsigned)a.cap_cache);
+  const unsigned vt_stride_s = __builtin_amdgcn_readfirstlane((unsigned)a.cap_stage);
+  auto copy_k = [&](int t, char *dst) {
+    const int nk = t * BN;
+    const char *src = nk < a.P8 ? kb_c + (long)nk * D * 2 : kb_s + (long)(nk - a.P8) * D * 2;
+#pragma unroll
+    for (int j = 0; j < G::KDMA; ++j) dma16(src + k_src(j), dst + (wave + j * NW) * 1024);
+  };
+  auto copy_v = [&](int t, char *dst) {
+    const int nk = t * BN;
+    const bool cached = nk < a.P8;
+    const char *src = cached ? vt_c + (long)nk * 2 : vt_s + (long)(nk - a.P8) * 2;
+    const unsigned stride = cached ? vt_stride_c : vt_stride_s;
+#pragma unroll
+    for (int j = 0; j < G::VDMA; ++j) dma16(src + v_src(j, stride), dst + (wave + j * NW) * 1024);
+  };
+
+  const int q_abs = a.P + wp0 + lq;
+  const int vis_hi = a.causal ? min(q_abs, key_total - 1) : key_total - 1;
+  const int vis_lo = a.window > 0 ? q_abs - a.window + 1 : 0;
+  const int wave_min_q = a.P + wp0;
+  const int wave_max_q = a.P + min(wp0 + 15, a.S - 1);
+  const int gk = 4 * g + 8 * (g >> 1);  // key16(b, 4g + i) = 32 (b >> 1) + 8 (b & 1) + i + gk
+  auto tile_masked = [&](int t) {
+    const int kt0 = t * BN;
+    return (a.causal && kt0 + BN - 1 > wave_min_q) || (a.window > 0 && kt0 + a.window <= wave_max_q) ||
+           (kt0 + BN > key_total);
+  };
+  // S^T of tile t into s (scaled score minus ms; -inf where masked).
+  auto score = [&](f32x4q (&s)[KB], const char *kbuf, int t) {
+    if (tile_masked(t)) {
+      const int kt0 = t * BN;
+      const int lo = vis_lo - kt0 - gk, hi = vis_hi - kt0 - gk;
+#pragma unroll
+      for (int b = 0; b < KB; ++b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int kk = 32 * (b >> 1) + 8 * (b & 1) + i;
+          s[b][i] = (kk < lo || kk > hi) ? NEG_INF : -ms;
+        }
+    } else {
+#pragma unroll
+      for (int b = 0; b < KB; ++b) s[b] = bias;
+    }
+#pragma unroll
+    for (int t2 = 0; t2 < DT; ++t2)
+#pragma unroll
+      for (int b = 0; b < KB; ++b) {
+        const bf16x8 kf = *reinterpret_cast<const bf16x8 *>(kbuf + (kbase[b] ^ (unsigned)(t2 << 6)));
+        s[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[t2], s[b], 0, 0, 0);
+      }
+  };
+
+  auto step = [&](auto O_, int t, f32x4q (&cur)[KB], f32x4q (&nxt)[KB]) {
+    constexpr int O = decltype(O_)::value;
+    char *const k_this = O ? k_lds1 : k_lds0;  // receives K(t+2)
+    char *const k_next = O ? k_lds0 : k_lds1;  // holds K(t+1)
+    char *const v_this = O ? v_lds1 : v_lds0;  // holds V(t)
+    char *const v_next = O ? v_lds0 : v_lds1;  // receives V(t+1)
+    if (t + 2 < t_end) copy_k(t + 2, k_this);
+    if (t + 1 < t_end) copy_v(t + 1, v_next);
+    score(nxt, k_next, t + 1);  // (reads a stale buffer on the last tile; ignored)
+
+    // probabilities of tile t, P^T for the PV B operand
+    bf16x8 pf[KS];
+    float psum = 0.0f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      bf16x8 p;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        p[i] = (bf16)fast_exp2(cur[2 * s][i]);
+        p[4 + i] = (bf16)fast_exp2(cur[2 * s + 1][i]);
+      }
+      psum += sum_bf16x8(p);
+      pf[s] = p;
+    }
+    const bool hot = (psum > kRaiseSum) | (m == NEG_INF);
+    if (__ballot(hot)) {
+      float v = cur[0][0];
+#pragma unroll
+      for (int b = 0; b < KB; ++b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v = vmax(v, cur[b][i]);
+      const float mx = xor32_max(xor16_max(v)) + ms;
+      const float mnew = mx > m ? mx : m;
+      const float msn = mnew == NEG_INF ? 0.0f : mnew;
+      const float shift = msn - ms;
+      const float alpha = fast_exp2(m - msn);  // 0 for a row that has seen no key
+      l *= alpha;
+#pragma unroll
+      for (int d = 0; d < DB; ++d) o[d] *= alpha;
+      psum = 0.0f;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        bf16x8 p;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          p[i] = (bf16)fast_exp2(cur[2 * s][i] - shift);
+          p[4 + i] = (bf16)fast_exp2(cur[2 * s + 1][i] - shift);
+        }
+        psum += sum_bf16x8(p);
+        pf[s] = p;
+      }
+#pragma unroll
+      for (int b = 0; b < KB; ++b) nxt[b] -= shift;
+      bias = f32x4q{-msn, -msn, -msn, -msn};
+      m = mnew;
+      ms = msn;
+    }
+    l += psum;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int d = 0; d < DB; ++d) {
+        const bf16x8 vf =
+            *reinterpret_cast<const bf16x8 *>(v_this + ((vbase ^ (unsigned)(s << 6)) + d * 16 * 2 * BN));
+        o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[s], o[d], 0, 0, 0);
+      }
+    wait_copies();
+    __syncthreads();
+  };
+
+  // Prologue: K(t0), V(t0), K(t0+1); S(t0).
+  f32x4q sa[KB], sb[KB];
+  copy_k(t_begin, k_lds0);
+  copy_v(t_begin, v_lds0);
+  if (t_begin + 1 < t_end) copy_k(t_begin + 1, k_lds1);
+  wait_copies();
+  __syncthreads();
+  score(sa, k_lds0, t_begin);
+  __syncthreads();  // every wave is done with K(t0) before K(t0+2) lands in its buffer
+
+  for (int t = t_begin; t < t_end; t += 2) {
+    step(std::integral_constant<int, 0>(), t, sa, sb);
+    if (t + 1 < t_end) step(std::integral_constant<int, 1>(), t + 1, sb, sa);
+  }
+
+  const float lt = xor32_sum(xor16_sum(l));
+  const int pos = wp0 + lq;
+  if (a.splits > 1) {
+    if (pos < a.S) {
+      const long row = ((long)split * a.S + pos) * a.Hq + head;
+      float *op = a.part_o + row * D + 4 * g;
+#pragma unroll
+      for (int d = 0; d < DB; ++d)
+        *reinterpret_cast<float4 *>(op + 16 * d) = make_float4(o[d][0], o[d][1], o[d][2], o[d][3]);
+      if (g == 0) {
+        a.part_ml[row * 2] = m;
+        a.part_ml[row * 2 + 1] = lt;
+      }
+    }
+    return;
+  }
+  if (pos < a.S) {
+    if (g == 0 && !(__float_as_uint(lt) - 1u < 0x7f7fffffu)) atomicOr(a.err, kDevErrSoftmaxDenominator);
+    const float inv = 1.0f / lt;
+    float *op = a.out + ((long)pos * a.Hq + head) * D + 4 * g;
+#pragma unroll
+    for (int d = 0; d < DB; ++d)
+      *reinterpret_cast<float4 *>(op + 16 * d) = make_float4(o[d][0] * inv, o[d][1] * inv, o[d][2] * inv, o[d][3] * inv);
+  }
+}
+
 namespace {
 
-template <int D, int RB, int NPB, int BN, int QB, int OS>
+template <int D, int RB, int NPB, int BN>
+hipError_t launch_q16(hipStream_t st, PrefillArgs a) {
+  constexpr int WGQ = NPB * 16;
+  a.n_qblocks = (a.S + WGQ - 1) / WGQ;
+  const long blocks = prefill_grid_workgroups(a.n_qblocks, a.R / RB, a.Hkv, a.splits, a.xcd_group);
+  hipLaunchKernelGGL((prefill_q16_kernel<D, RB, NPB, BN>), dim3((unsigned)blocks), dim3(RB * NPB * 64), 0, st, a);
+  return hipGetLastError();
+}
+
+template <int D, int RB, int NPB, int BN, int QB>
 hipError_t launch_shape(hipStream_t st, PrefillArgs a) {
   constexpr int WGQ = NPB * QB * 32;
   a.n_qblocks = (a.S + WGQ - 1) / WGQ;
   const long blocks = prefill_grid_workgroups(a.n_qblocks, a.R / RB, a.Hkv, a.splits, a.xcd_group);
-  hipLaunchKernelGGL((prefill_kernel<D, RB, NPB, BN, QB, OS>), dim3((unsigned)blocks), dim3(RB * NPB * OS * 64), 0,
+  hipLaunchKernelGGL((prefill_kernel<D, RB, NPB, BN, QB>), dim3((unsigned)blocks), dim3(RB * NPB * 64), 0,
                      st, a);
   return hipGetLastError();
 }
 
-// Four-wave workgroups (eight with the O split), 32 queries per wave, 64-key
-// tiles (32 at head_dim 256), two waves per SIMD (one at head_dim 256 without
-// the O split): four heads of the KV group,
-// two heads with two blocks, or one head with four blocks. (64 queries per
-// wave halves the LDS fragment reads per
+// Four-wave workgroups of 32 queries per wave, 64-key tiles, two waves per
+// SIMD: four heads of the KV group, two heads with two blocks, or one head
+// with four blocks. (64 queries per wave halves the LDS fragment reads per
 // MFMA but, at head_dim 128, needs more than 256 VGPRs and measured slower;
 // at head_dim 64 it halves the workgroup count, which a 2048-token prefill
-// cannot afford.) Windowed head_dim-256 layers run half-size workgroups (two
-// heads, or one head with two blocks): their short key ranges leave CUs idle
-// with the full size (Gemma-3-1B's W512 layer 43.1 -> 40.5 us, Gemma-3-4B's
-// W1024 chunk 30.6 -> 27.7 us), while the long causal ranges of the global
-// layers run 30-40% slower with them.
-template <int D, int BN, int OS>
+// cannot afford.)
+template <int D>
 hipError_t launch_r(hipStream_t st, const PrefillArgs &a) {
-  if constexpr (D >= 256) {
-    if (prefill_half_wg(a, D)) {
-      if (a.R % 2 == 0) return launch_shape<D, 2, 1, BN, 1, OS>(st, a);
-      return launch_shape<D, 1, 2, BN, 1, OS>(st, a);
-    }
-  }
-  if (a.R % 4 == 0) return launch_shape<D, 4, 1, BN, 1, OS>(st, a);
-  if (a.R % 2 == 0) return launch_shape<D, 2, 2, BN, 1, OS>(st, a);
-  return launch_shape<D, 1, 4, BN, 1, OS>(st, a);
+  constexpr int BN = 64;
+  if (a.R % 4 == 0) return launch_shape<D, 4, 1, BN, 1>(st, a);
+  if (a.R % 2 == 0) return launch_shape<D, 2, 2, BN, 1>(st, a);
+  return launch_shape<D, 1, 4, BN, 1>(st, a);
+}
+
+// head_dim 256: four waves of 16 queries, 32-key tiles: four heads, two heads
+// with two blocks, or one head with four blocks.
+template <int D>
+hipError_t launch_r16(hipStream_t st, const PrefillArgs &a) {
+  constexpr int BN = 32;
+  if (a.R % 4 == 0) return launch_q16<D, 4, 1, BN>(st, a);
+  if (a.R % 2 == 0) return launch_q16<D, 2, 2, BN>(st, a);
+  return launch_q16<D, 1, 4, BN>(st, a);
 }
 
 template <int D>
 hipError_t launch_d(hipStream_t st, const PrefillArgs &a) {
-  constexpr int BN = D >= 256 ? 32 : 64;  // head_dim 256: 32-key tiles
-  if constexpr (D >= 256) {
-    // one wave per SIMD; with O split over two waves, two (for long ranges)
-    if (a.o_split) return launch_r<D, BN, 2>(st, a);
-  }
-  return launch_r<D, BN, 1>(st, a);
+  if constexpr (D >= 256) return launch_r16<D>(st, a);
+  else return launch_r<D>(st, a);
 }
 
 }  // namespace
@@ -754,18 +1004,12 @@ hipError_t launch_d(hipStream_t st, const PrefillArgs &a) {
 
 bool prefill_supported(int D) { return D == 64 || D == 128 || D == 256; }
 
-// Workgroups of 32 queries per wave (launch_r above): four heads x 32
-// queries, two heads x 64, or one head x 128; half-size ones two heads x 32
-// or one head x 64.
-bool prefill_half_wg(const PrefillArgs &a, int D) { return D >= 256 && a.window > 0; }
-int prefill_wg_heads(const PrefillArgs &a, int D) {
-  if (prefill_half_wg(a, D)) return a.R % 2 == 0 ? 2 : 1;
-  return a.R % 4 == 0 ? 4 : a.R % 2 == 0 ? 2 : 1;
-}
-int prefill_wg_queries(const PrefillArgs &a, int D) {
-  return (prefill_half_wg(a, D) ? 64 : 128) / prefill_wg_heads(a, D);
-}
-int prefill_wgs_per_cu(int D) { return D >= 256 ? 1 : 2; }
+// Workgroups of four waves (launch_r, launch_r16 above): four heads, two
+// heads with two query blocks, or one head with four blocks; a wave's block is
+// 32 queries (16 at head_dim 256), so a workgroup covers 128 query rows (64).
+int prefill_wg_heads(const PrefillArgs &a, int) { return a.R % 4 == 0 ? 4 : a.R % 2 == 0 ? 2 : 1; }
+int prefill_wg_queries(const PrefillArgs &a, int D) { return (D >= 256 ? 64 : 128) / prefill_wg_heads(a, D); }
+int prefill_wgs_per_cu(int) { return 2; }
 int prefill_tile_keys(int D) { return D >= 256 ? 32 : 64; }  // BN of launch_d
 
 long prefill_base_workgroups(const PrefillArgs &a, int D) {

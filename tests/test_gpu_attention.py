@@ -170,6 +170,29 @@ def test_prefill_reference_rises_across_tiles(gpu, D, Hq, Hkv):
     assert rel_err(got[lo:], ref[lo:]) <= BF16_TOL
 
 
+@pytest.mark.parametrize("D,Hq,Hkv", [(64, 8, 2), (128, 6, 2), (256, 4, 1)])
+def test_prefill_rows_first_seeing_keys_far_below_zero(gpu, D, Hq, Hkv):
+    """Windowed causal prefill whose scores all sit about 130 log2 units below
+    zero: the rows whose window starts past a workgroup's first key tile have
+    accumulated nothing (m = -inf) when their first visible keys arrive, and
+    their rescale factor must be 0, not 2^130 (0 x inf = NaN). The common
+    score offset comes from dim 0 set to +-amp in q and k, exact in bf16, so
+    the bf16 scores stay accurate relative to each other."""
+    S, W = 320, 100
+    amp = 40.0 if D <= 128 else 48.0  # amp^2 / sqrt(D) x log2(e) > 128; exact in bf16
+    print(f"[case] prefill far-negative scores D={D} Hq={Hq} Hkv={Hkv} S={S} W={W}", flush=True)
+    q, k, v, _, _ = layer_inputs(29, D, S, 0, Hq, Hkv, D)
+    q = q.reshape(S, Hq, D)
+    k = k.reshape(S, Hkv, D)
+    q[:, :, 0] = amp
+    k[:, :, 0] = -amp  # every score gets -amp^2 / sqrt(D)
+    q, k = q.ravel().copy(), k.ravel().copy()
+    ref = o.sdpa_with_cache(q, k, v, None, S, Hq, Hkv, D, True, W)
+    got = gpu.scaled_dot_product_attention_with_cache(q, k, v, None, gpu.KvAttentionConfig(S, Hq, Hkv, D, True, W))
+    assert np.all(np.isfinite(got))
+    assert rel_err(got, ref) <= BF16_TOL
+
+
 def test_invalid_softmax_denominator_is_reported(gpu):
     P, Hq, Hkv, D = 64, 8, 2, 128
     q, k, v, pk, pv = layer_inputs(16, 0, 1, P, Hq, Hkv, D)

@@ -125,8 +125,8 @@ def check_prefill(cfg, P, plan):
     key_total = P + S
     n_qblocks = -(-S // WGQ)
     rb = plan["heads_per_block"]
-    # 32 queries per wave, four waves per workgroup (two: windowed head_dim 256)
-    assert rb * WGQ == (64 if D >= 256 and W > 0 else 128)
+    # four waves per workgroup of 32 queries each (16 at head_dim 256)
+    assert rb * WGQ == (64 if D >= 256 else 128)
     assert plan["head_blocks"] * rb == Hq // Hkv
     check_prefill_grid(plan, n_qblocks, Hkv, plan["head_blocks"], splits)
     P8 = P & ~(TILE_ALIGN - 1)
