@@ -509,7 +509,10 @@ hipError_t launch_one(hipStream_t st, const DecodeArgs &a) {
   if (a.max_splits < 1) return hipErrorInvalidValue;  // the new token needs a split
   {
     dim3 grid((unsigned)(a.Hkv * a.HB), (unsigned)a.max_splits, (unsigned)a.B);
-    hipLaunchKernelGGL((decode_split_kernel<D, RB, rows_per_group(RB)>), grid, dim3(256), 0, st, a);
+    if (a.kps < 4 * (64 / (D / 8)) * rows_per_group(RB))  // small layers: one row per group
+      hipLaunchKernelGGL((decode_split_kernel<D, RB, 1>), grid, dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL((decode_split_kernel<D, RB, rows_per_group(RB)>), grid, dim3(256), 0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -545,6 +548,10 @@ int decode_keys_per_split(int D, int RB, long total_rows, int max_keys, int spli
   const long per = (total_rows + target - 1) / target;
   long kps = ((per + chunk - 1) / chunk) * chunk;
   if (kps < chunk) kps = chunk;
+  // Small layers (fewer keys per workgroup than one iteration's worth): one
+  // row per lane group, so the grid has twice or three times the workgroups
+  // (Llama-3.2-1B at 512 keys: 7.38 -> 6.99 us per layer).
+  if (per < chunk) kps = std::max<long>(chunk / rows_per_group(RB), per);
   // Bound the partials the combine kernel reads per output (and the caller's
   // partial buffer).
   const long cap = std::max(1, std::min(split_cap, kMaxDecodeSplits));
