@@ -1131,7 +1131,7 @@ static void plan_prefill(PrefillArgs &a, int D, int cus, PrefillPlan *p) {
   // splits cover the widest tile range any workgroup has, so every
   // workgroup's keys are covered.
   const long base = prefill_base_workgroups(a, D);
-  const long slots = (long)cus * prefill_wgs_per_cu(D);
+  const long slots = (long)cus * prefill_wgs_per_cu(a, D);
   p->tiles = prefill_max_tile_span(a, D);
   if (base < slots) {
     const long want = std::min(std::min((slots + base - 1) / base, p->tiles / 4), (long)D);

@@ -550,8 +550,13 @@ int decode_keys_per_split(int D, int RB, long total_rows, int max_keys, int spli
   if (kps < chunk) kps = chunk;
   // Small layers (fewer keys per workgroup than one iteration's worth): one
   // row per lane group, so the grid has twice or three times the workgroups
-  // (Llama-3.2-1B at 512 keys: 7.38 -> 6.99 us per layer).
-  if (per < chunk) kps = std::max<long>(chunk / rows_per_group(RB), per);
+  // (Llama-3.2-1B at 512 keys: 7.38 -> 6.99 us per layer), unless that takes
+  // the combine past its narrow form (Gemma-3-4B's W1024 layer at 128 splits:
+  // 7.7 -> 9.6 us).
+  if (per < chunk) {
+    const long small = std::max<long>(chunk / rows_per_group(RB), per);
+    if ((max_keys + small - 1) / small < kCombineWideSplits) kps = small;
+  }
   // Bound the partials the combine kernel reads per output (and the caller's
   // partial buffer).
   const long cap = std::max(1, std::min(split_cap, kMaxDecodeSplits));

@@ -128,7 +128,7 @@ struct PrefillArgs {
 
 // Workgroup slots per CU and key-tile width of the prefill kernels, and the
 // queries per workgroup, for choosing key splits.
-int prefill_wgs_per_cu(int D);
+int prefill_wgs_per_cu(const PrefillArgs &a, int D);
 int prefill_tile_keys(int D);
 int prefill_wg_queries(const PrefillArgs &a, int D);
 int prefill_wg_heads(const PrefillArgs &a, int D);  // query heads per workgroup

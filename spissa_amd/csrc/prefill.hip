@@ -98,9 +98,45 @@ __device__ __forceinline__ void dma16(const char *src, char *lds_base) {
   __builtin_amdgcn_global_load_lds(src, (lds_void *)lds_base, 16, 0, 0);
 }
 
+// dma16 issued as inline assembly. The compiler then tracks no copy into LDS
+// and inserts no wait of its own before LDS reads (it cannot tell which stage a
+// copy fills once control flow merges); the kernel waits for exactly the
+// copies it reads with wait_copies_upto. The compiler's own vmcnt waits for
+// its loads stay correct: copies complete in issue order, and copies it does
+// not count only make a wait for an earlier load stricter.
+// base is wave-uniform (an SGPR pair), off the lane's byte offset from it.
+__device__ __forceinline__ void dma16_untracked(const char *base, unsigned off, char *lds_base) {
+  const unsigned lds = (unsigned)(uintptr_t)(lds_void *)lds_base;
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
+}
+
 // Waits for this wave's outstanding global -> LDS copies.
 __device__ __forceinline__ void wait_copies() {
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt and lgkmcnt unconstrained
+}
+
+// Workgroup barrier that orders LDS accesses but, unlike __syncthreads(), lets
+// this wave's global -> LDS copies stay in flight (the workgroup fence there
+// waits for all of them). The caller waits for the copies the next step reads
+// (wait_copies, wait_copies_upto); lgkmcnt(0) retires this wave's LDS reads
+// before another wave's copy may overwrite what they read.
+__device__ __forceinline__ void copies_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Waits until at most n of this wave's global -> LDS copies are outstanding
+// (they complete in issue order). n is wave-uniform; the wait uses the largest
+// multiple of STEP not above n or MAX.
+template <int MAX, int STEP>
+__device__ __forceinline__ void wait_copies_upto(int n) {
+  static_assert(MAX < 64, "vmcnt holds 6 bits");
+  if constexpr (MAX <= 0) {
+    wait_copies();
+  } else {
+    if (n >= MAX) {
+      __builtin_amdgcn_s_waitcnt(0x0F70 | (MAX & 15) | ((MAX >> 4) << 14));
+      return;
+    }
+    wait_copies_upto<MAX - STEP, STEP>(n);
+  }
 }
 
 // XOR swizzle of a row of NC 16-byte chunks (NC = 4, 8, 16 or 32), staying below
@@ -650,17 +686,20 @@ __device__ __forceinline__ float xor16_sum(float v) {
 
 // The head_dim-256 prefill: waves of 16 queries on v_mfma_f32_16x16x32_bf16.
 // A wave holds the whole head dim of its 16 queries (O^T 64 VGPRs, Q^T 32), so
-// no O split or score exchange between waves is needed and two four-wave
-// workgroups share a CU. RB heads x NPB blocks of 16 queries per workgroup,
-// BN-key tiles, the same copies, masks, pipeline and key splits as
-// prefill_kernel, lazy exponent reference.
+// no O split or score exchange between waves is needed. RB heads x NPB blocks
+// of 16 queries per workgroup, BN-key tiles, the masks and key splits of
+// prefill_kernel, lazy exponent reference. NST K and V^T stages of LDS: two
+// (two workgroups per CU) with the step order of prefill_kernel, or four (one
+// per CU) with DEEP, a software-pipelined step (fragment reads ahead of the
+// MFMAs, copies spread among them) for a lone wave per SIMD.
 //   S^T = K Q^T   A = 16 key rows x 32 dims from LDS (rows key16(b, lane %
 //                 16)), B = Q^T in registers; lane l holds keys key16(b,
 //                 4 (l / 16) + i) of query l % 16;
 //   O^T += V^T P^T  A = 16 dim rows x 32 V^T slots from LDS, B = P^T from
 //                 the score registers (key16 makes them the slots' keys).
-template <int D, int RB, int NPB, int BN>
-__global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_q16_kernel(const PrefillArgs a) {
+template <int D, int RB, int NPB, int BN, int NST, bool DEEP>
+__global__ __launch_bounds__(RB *NPB * 64, NST > 2 ? 1 : 2) void prefill_q16_kernel(const PrefillArgs a) {
+  static_assert(NST == 2 || NST == 4, "the step loop alternates two score buffers over NST stages");
   constexpr int NW = RB * NPB;
   constexpr int WGQ = NPB * 16;
   using G = Geom<D, BN, NW>;
@@ -670,10 +709,32 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_q16_kernel(const Pref
   constexpr int DB = D / 16;   // 16-dim output blocks
   static_assert(D >= 128 && D / 8 >= 16, "swz_k16 needs 16 chunks per K row");
 
+  // One named array per stage: the compiler then sees that a read of one stage
+  // does not alias the copies into another and waits for no copy before it.
+  constexpr int KB2 = NST > 2 ? G::KBYTES : 16, VB2 = NST > 2 ? G::VBYTES : 16;
   __shared__ __attribute__((aligned(1024))) char k_lds0[G::KBYTES];
   __shared__ __attribute__((aligned(1024))) char k_lds1[G::KBYTES];
+  __shared__ __attribute__((aligned(1024))) char k_lds2[KB2];
+  __shared__ __attribute__((aligned(1024))) char k_lds3[KB2];
   __shared__ __attribute__((aligned(1024))) char v_lds0[G::VBYTES];
   __shared__ __attribute__((aligned(1024))) char v_lds1[G::VBYTES];
+  __shared__ __attribute__((aligned(1024))) char v_lds2[VB2];
+  __shared__ __attribute__((aligned(1024))) char v_lds3[VB2];
+  auto k_lds = [&](auto I_) -> char * {
+    constexpr int I = decltype(I_)::value % NST;
+    if constexpr (I == 0) return k_lds0;
+    else if constexpr (I == 1) return k_lds1;
+    else if constexpr (I == 2) return k_lds2;
+    else return k_lds3;
+  };
+  auto v_lds = [&](auto I_) -> char * {
+    constexpr int I = decltype(I_)::value % NST;
+    if constexpr (I == 0) return v_lds0;
+    else if constexpr (I == 1) return v_lds1;
+    else if constexpr (I == 2) return v_lds2;
+    else return v_lds3;
+  };
+  using I0 = std::integral_constant<int, 0>;
 
   const int HB = a.R / RB;
   int h, hb, split, qt;
@@ -790,7 +851,7 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_q16_kernel(const Pref
     const int nk = t * BN;
     const char *src = nk < a.P8 ? kb_c + (long)nk * D * 2 : kb_s + (long)(nk - a.P8) * D * 2;
 #pragma unroll
-    for (int j = 0; j < G::KDMA; ++j) dma16(src + k_src(j), dst + (wave + j * NW) * 1024);
+    for (int j = 0; j < G::KDMA; ++j) dma16_untracked(src, k_src(j), dst + (wave + j * NW) * 1024);
   };
   auto copy_v = [&](int t, char *dst) {
     const int nk = t * BN;
@@ -798,7 +859,21 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_q16_kernel(const Pref
     const char *src = cached ? vt_c + (long)nk * 2 : vt_s + (long)(nk - a.P8) * 2;
     const unsigned stride = cached ? vt_stride_c : vt_stride_s;
 #pragma unroll
-    for (int j = 0; j < G::VDMA; ++j) dma16(src + v_src(j, stride), dst + (wave + j * NW) * 1024);
+    for (int j = 0; j < G::VDMA; ++j) dma16_untracked(src, v_src(j, stride), dst + (wave + j * NW) * 1024);
+  };
+  // Copy j (of KDMA + VDMA) of this wave's share of K(tk) and V(tv).
+  auto copy_kv1 = [&](int tk, char *kdst, int tv, char *vdst, int j) {
+    if (j < G::KDMA) {
+      const int nk = tk * BN;
+      const char *src = nk < a.P8 ? kb_c + (long)nk * D * 2 : kb_s + (long)(nk - a.P8) * D * 2;
+      dma16_untracked(src, k_src(j), kdst + (wave + j * NW) * 1024);
+    } else {
+      const int nk = tv * BN;
+      const bool cached = nk < a.P8;
+      const char *src = cached ? vt_c + (long)nk * 2 : vt_s + (long)(nk - a.P8) * 2;
+      const unsigned stride = cached ? vt_stride_c : vt_stride_s;
+      dma16_untracked(src, v_src(j - G::KDMA, stride), vdst + (wave + (j - G::KDMA) * NW) * 1024);
+    }
   };
 
   const int q_abs = a.P + wp0 + lq;
@@ -812,8 +887,9 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_q16_kernel(const Pref
     return (a.causal && kt0 + BN - 1 > wave_min_q) || (a.window > 0 && kt0 + a.window <= wave_max_q) ||
            (kt0 + BN > key_total);
   };
-  // S^T of tile t into s (scaled score minus ms; -inf where masked).
-  auto score = [&](f32x4q (&s)[KB], const char *kbuf, int t) {
+  // S^T of tile t into s (scaled score minus ms; -inf where masked): the
+  // accumulators' start values, then the MFMAs.
+  auto score_init = [&](f32x4q (&s)[KB], int t) {
     if (tile_masked(t)) {
       const int kt0 = t * BN;
       const int lo = vis_lo - kt0 - gk, hi = vis_hi - kt0 - gk;
@@ -828,24 +904,60 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_q16_kernel(const Pref
 #pragma unroll
       for (int b = 0; b < KB; ++b) s[b] = bias;
     }
+  };
+  // Fragment i of the K tile (dim step i / KB, block i % KB) and of the V^T
+  // tile (32-key step i / DB, dim block i % DB).
+  auto read_k = [&](const char *kbuf, int i) {
+    return *reinterpret_cast<const bf16x8 *>(kbuf + (kbase[i % KB] ^ (unsigned)((i / KB) << 6)));
+  };
+  auto read_v = [&](const char *vbuf, int i) {
+    return *reinterpret_cast<const bf16x8 *>(vbuf + ((vbase ^ (unsigned)((i / DB) << 6)) + (i % DB) * 16 * 2 * BN));
+  };
+  auto score = [&](f32x4q (&s)[KB], const char *kbuf, int t) {
+    score_init(s, t);
 #pragma unroll
-    for (int t2 = 0; t2 < DT; ++t2)
-#pragma unroll
-      for (int b = 0; b < KB; ++b) {
-        const bf16x8 kf = *reinterpret_cast<const bf16x8 *>(kbuf + (kbase[b] ^ (unsigned)(t2 << 6)));
-        s[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[t2], s[b], 0, 0, 0);
-      }
+    for (int i = 0; i < DT * KB; ++i)
+      s[i % KB] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(read_k(kbuf, i), qf[i / KB], s[i % KB], 0, 0, 0);
   };
 
-  auto step = [&](auto O_, int t, f32x4q (&cur)[KB], f32x4q (&nxt)[KB]) {
-    constexpr int O = decltype(O_)::value;
-    char *const k_this = O ? k_lds1 : k_lds0;  // receives K(t+2)
-    char *const k_next = O ? k_lds0 : k_lds1;  // holds K(t+1)
-    char *const v_this = O ? v_lds1 : v_lds0;  // holds V(t)
-    char *const v_next = O ? v_lds0 : v_lds1;  // receives V(t+1)
-    if (t + 2 < t_end) copy_k(t + 2, k_this);
-    if (t + 1 < t_end) copy_v(t + 1, v_next);
-    score(nxt, k_next, t + 1);  // (reads a stale buffer on the last tile; ignored)
+  // K(j) and V(j) live in stage (j - t_begin) % NST. Step t copies K(t + NST)
+  // into K(t)'s stage (its scores were taken one step earlier) and V(t + NST -
+  // 1) into V(t - 1)'s stage, and needs K(t + 1) and V(t) landed; at its end it
+  // waits for K(t + 2) and V(t + 1) only. In copy order the pairs are K(t0),
+  // then (K(t0 + k), V(t0 + k - 1)) for k = 1, 2, ...; pending(t, k0, k1) counts
+  // this wave's copies in pairs (K(t + k), V(t + k - 1)), k0 <= k <= k1.
+  static_assert(G::KDMA == G::VDMA, "pending() counts K and V copies in equal groups");
+  // Deep steps: software-pipelined, PF fragment pairs read ahead (4, 6 and 8
+  // measured alike).
+  constexpr int PF = 4;
+  static_assert(!DEEP || DT * KB == KS * DB, "deep steps pair K and V fragments");
+  auto pending = [&](int t, int k0, int k1) {
+    int n = 0;
+#pragma unroll
+    for (int k = k0; k <= k1; ++k) n += (t + k < t_end ? G::KDMA : 0) + (t + k - 1 < t_end ? G::VDMA : 0);
+    return n;
+  };
+  auto step = [&](auto Ph_, int t, f32x4q (&cur)[KB], f32x4q (&nxt)[KB]) {
+    constexpr int Ph = decltype(Ph_)::value;  // (t - t_begin) % NST
+    char *const k_next = k_lds(std::integral_constant<int, Ph + 1>());  // holds K(t+1)
+    char *const v_this = v_lds(Ph_);                                    // holds V(t)
+    // (the scores of tile t + 1 read a stale buffer on the last tile; ignored)
+    constexpr int NF = DT * KB;  // fragments of each kind per step
+    bf16x8 kf[DEEP ? NF : 1], vf[DEEP ? NF : 1];
+    if constexpr (DEEP) {
+      // Software pipeline for one wave per SIMD: fragment reads run PF pairs
+      // ahead of their MFMAs and the step's copies are spread over the MFMAs,
+      // so the LDS, the copy path and the matrix unit work at the same time.
+#pragma unroll
+      for (int i = 0; i < PF; ++i) {
+        kf[i] = read_k(k_next, i);
+        vf[i] = read_v(v_this, i);
+      }
+    } else {
+      if (t + NST < t_end) copy_k(t + NST, k_lds(Ph_));
+      if (t + NST - 1 < t_end) copy_v(t + NST - 1, v_lds(std::integral_constant<int, Ph + NST - 1>()));
+      score(nxt, k_next, t + 1);
+    }
 
     // probabilities of tile t, P^T for the PV B operand
     bf16x8 pf[KS];
@@ -888,38 +1000,76 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_q16_kernel(const Pref
         psum += sum_bf16x8(p);
         pf[s] = p;
       }
+      if constexpr (!DEEP) {
 #pragma unroll
-      for (int b = 0; b < KB; ++b) nxt[b] -= shift;
+        for (int b = 0; b < KB; ++b) nxt[b] -= shift;
+      }
       bias = f32x4q{-msn, -msn, -msn, -msn};
       m = mnew;
       ms = msn;
     }
     l += psum;
+    if constexpr (DEEP) {
+      score_init(nxt, t + 1);  // (after the reference update: no shift of nxt needed)
+      // Every step copies K(t + NST) and V(t + NST - 1), clamped to the last
+      // tile past the range (into stages no later step reads), so the waits
+      // count a fixed number of copies.
+      const int tk = min(t + NST, t_end - 1), tv = min(t + NST - 1, t_end - 1);
+      char *const kdst = k_lds(Ph_);
+      char *const vdst = v_lds(std::integral_constant<int, Ph + NST - 1>());
+      constexpr int NC = G::KDMA + G::VDMA;
+      static_assert(NF % NC == 0, "copies spread evenly over the MFMA pairs");
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
-#pragma unroll
-      for (int d = 0; d < DB; ++d) {
-        const bf16x8 vf =
-            *reinterpret_cast<const bf16x8 *>(v_this + ((vbase ^ (unsigned)(s << 6)) + d * 16 * 2 * BN));
-        o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[s], o[d], 0, 0, 0);
+      for (int i = 0; i < NF; ++i) {
+        nxt[i % KB] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[i], qf[i / KB], nxt[i % KB], 0, 0, 0);
+        o[i % DB] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[i], pf[i / DB], o[i % DB], 0, 0, 0);
+        if (i + PF < NF) {
+          kf[i + PF] = read_k(k_next, i + PF);
+          vf[i + PF] = read_v(v_this, i + PF);
+        }
+        if (i % (NF / NC) == NF / NC - 1) copy_kv1(tk, kdst, tv, vdst, i / (NF / NC));
       }
-    wait_copies();
-    __syncthreads();
+    } else {
+#pragma unroll
+      for (int i = 0; i < KS * DB; ++i)
+        o[i % DB] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(read_v(v_this, i), pf[i / DB], o[i % DB], 0, 0, 0);
+    }
+    if constexpr (DEEP) wait_copies_upto<(NST - 2) * 2 * G::KDMA, G::KDMA>((NST - 2) * 2 * G::KDMA);
+    else wait_copies_upto<(NST - 2) * 2 * G::KDMA, G::KDMA>(pending(t, 3, NST));
+    copies_barrier();
   };
 
-  // Prologue: K(t0), V(t0), K(t0+1); S(t0).
+  // Prologue: K(t0) .. K(t0 + NST - 1), V(t0) .. V(t0 + NST - 2); S(t0).
   f32x4q sa[KB], sb[KB];
-  copy_k(t_begin, k_lds0);
-  copy_v(t_begin, v_lds0);
-  if (t_begin + 1 < t_end) copy_k(t_begin + 1, k_lds1);
-  wait_copies();
-  __syncthreads();
-  score(sa, k_lds0, t_begin);
-  __syncthreads();  // every wave is done with K(t0) before K(t0+2) lands in its buffer
+  copy_k(t_begin, k_lds(I0()));
+  auto prologue_pair = [&](auto K_) {
+    constexpr int k = decltype(K_)::value;
+    if constexpr (k < NST) {
+      if constexpr (DEEP) {  // (clamped as in the steps)
+        copy_k(min(t_begin + k, t_end - 1), k_lds(K_));
+        copy_v(min(t_begin + k - 1, t_end - 1), v_lds(std::integral_constant<int, k - 1>()));
+      } else {
+        if (t_begin + k < t_end) copy_k(t_begin + k, k_lds(K_));
+        if (t_begin + k - 1 < t_end) copy_v(t_begin + k - 1, v_lds(std::integral_constant<int, k - 1>()));
+      }
+    }
+  };
+  prologue_pair(std::integral_constant<int, 1>());
+  prologue_pair(std::integral_constant<int, 2>());
+  prologue_pair(std::integral_constant<int, 3>());
+  wait_copies_upto<(NST - 1) * 2 * G::KDMA, G::KDMA>(DEEP ? (NST - 1) * 2 * G::KDMA : pending(t_begin, 1, NST - 1));
+  copies_barrier();
+  score(sa, k_lds(I0()), t_begin);
+  wait_copies_upto<(NST - 2) * 2 * G::KDMA, G::KDMA>(DEEP ? (NST - 2) * 2 * G::KDMA : pending(t_begin, 2, NST - 1));
+  copies_barrier();  // K(t0+1) and V(t0) landed; every wave is done with K(t0) before K(t0+NST) lands there
 
-  for (int t = t_begin; t < t_end; t += 2) {
+  for (int t = t_begin; t < t_end; t += NST) {
     step(std::integral_constant<int, 0>(), t, sa, sb);
     if (t + 1 < t_end) step(std::integral_constant<int, 1>(), t + 1, sb, sa);
+    if constexpr (NST == 4) {
+      if (t + 2 < t_end) step(std::integral_constant<int, 2>(), t + 2, sa, sb);
+      if (t + 3 < t_end) step(std::integral_constant<int, 3>(), t + 3, sb, sa);
+    }
   }
 
   const float lt = xor32_sum(xor16_sum(l));
@@ -950,12 +1100,13 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_q16_kernel(const Pref
 
 namespace {
 
-template <int D, int RB, int NPB, int BN>
+template <int D, int RB, int NPB, int BN, int NST, bool DEEP>
 hipError_t launch_q16(hipStream_t st, PrefillArgs a) {
   constexpr int WGQ = NPB * 16;
   a.n_qblocks = (a.S + WGQ - 1) / WGQ;
   const long blocks = prefill_grid_workgroups(a.n_qblocks, a.R / RB, a.Hkv, a.splits, a.xcd_group);
-  hipLaunchKernelGGL((prefill_q16_kernel<D, RB, NPB, BN>), dim3((unsigned)blocks), dim3(RB * NPB * 64), 0, st, a);
+  hipLaunchKernelGGL((prefill_q16_kernel<D, RB, NPB, BN, NST, DEEP>), dim3((unsigned)blocks), dim3(RB * NPB * 64), 0,
+                     st, a);
   return hipGetLastError();
 }
 
@@ -985,12 +1136,20 @@ hipError_t launch_r(hipStream_t st, const PrefillArgs &a) {
 
 // head_dim 256: four waves of 16 queries, 32-key tiles: four heads, two heads
 // with two blocks, or one head with four blocks.
+template <int D, int NST, bool DEEP>
+hipError_t launch_r16n(hipStream_t st, const PrefillArgs &a) {
+  constexpr int BN = 32;
+  if (a.R % 4 == 0) return launch_q16<D, 4, 1, BN, NST, DEEP>(st, a);
+  if (a.R % 2 == 0) return launch_q16<D, 2, 2, BN, NST, DEEP>(st, a);
+  return launch_q16<D, 1, 4, BN, NST, DEEP>(st, a);
+}
+// Windowed layers (one workgroup per CU at Gemma-3-1B's 4096 tokens): four
+// stages and the software-pipelined step. Full causal layers: two stages and
+// two workgroups per CU, where the pipelined step measured slower.
 template <int D>
 hipError_t launch_r16(hipStream_t st, const PrefillArgs &a) {
-  constexpr int BN = 32;
-  if (a.R % 4 == 0) return launch_q16<D, 4, 1, BN>(st, a);
-  if (a.R % 2 == 0) return launch_q16<D, 2, 2, BN>(st, a);
-  return launch_q16<D, 1, 4, BN>(st, a);
+  if (a.window > 0) return launch_r16n<D, 4, true>(st, a);
+  return launch_r16n<D, 2, false>(st, a);
 }
 
 template <int D>
@@ -1009,7 +1168,8 @@ bool prefill_supported(int D) { return D == 64 || D == 128 || D == 256; }
 // 32 queries (16 at head_dim 256), so a workgroup covers 128 query rows (64).
 int prefill_wg_heads(const PrefillArgs &a, int) { return a.R % 4 == 0 ? 4 : a.R % 2 == 0 ? 2 : 1; }
 int prefill_wg_queries(const PrefillArgs &a, int D) { return (D >= 256 ? 64 : 128) / prefill_wg_heads(a, D); }
-int prefill_wgs_per_cu(int) { return 2; }
+// Windowed head_dim-256 layers run the four-stage kernel (128 KB of LDS).
+int prefill_wgs_per_cu(const PrefillArgs &a, int D) { return D >= 256 && a.window > 0 ? 1 : 2; }
 int prefill_tile_keys(int D) { return D >= 256 ? 32 : 64; }  // BN of launch_d
 
 long prefill_base_workgroups(const PrefillArgs &a, int D) {
