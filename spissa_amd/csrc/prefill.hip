@@ -354,7 +354,7 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
     const int nk = t * BN;
     const char *src = nk < a.P8 ? kb_c + (long)nk * D * 2 : kb_s + (long)(nk - a.P8) * D * 2;
 #pragma unroll
-    for (int j = 0; j < G::KDMA; ++j) dma16(src + k_src(j), dst + (wave + j * NW) * 1024);
+    for (int j = 0; j < G::KDMA; ++j) dma16_untracked(src, k_src(j), dst + (wave + j * NW) * 1024);
   };
   auto copy_v = [&](int t, char *dst) {
     const int nk = t * BN;
@@ -362,7 +362,7 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
     const char *src = cached ? vt_c + (long)nk * 2 : vt_s + (long)(nk - a.P8) * 2;
     const unsigned stride = cached ? vt_stride_c : vt_stride_s;
 #pragma unroll
-    for (int j = 0; j < G::VDMA; ++j) dma16(src + v_src(j, stride), dst + (wave + j * NW) * 1024);
+    for (int j = 0; j < G::VDMA; ++j) dma16_untracked(src, v_src(j, stride), dst + (wave + j * NW) * 1024);
   };
 
   // Visible keys [vis_lo, vis_hi] of this lane's two queries.
@@ -568,7 +568,7 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
       }
     }
     wait_copies();
-    __syncthreads();
+    copies_barrier();
   };
 
   // Prologue: K(t0), V(t0), K(t0+1) copied; S(t0) and its row maxima.
@@ -577,7 +577,7 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
   copy_v(t_begin, v_lds0);
   if (t_begin + 1 < t_end) copy_k(t_begin + 1, k_lds1);
   wait_copies();
-  __syncthreads();
+  copies_barrier();
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     ms[qb] = 0.0f;
@@ -601,7 +601,7 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
       for (int i = 0; i < 16; ++i) bias[qb][i] = -ms[qb];
     }
   }
-  __syncthreads();  // every wave is done with K(t0) before K(t0+2) lands in its buffer
+  copies_barrier();  // every wave is done with K(t0) before K(t0+2) lands in its buffer
 
   for (int t = t_begin; t < t_end; t += 2) {
     step(std::integral_constant<int, 0>(), t, sa, sb);
