@@ -281,28 +281,32 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
   // Q^T (B operand): lane holds query lq of block qb, dims 16t + 8hl + [0,8).
   // Q carries the softmax scale times log2(e), so the scores come out of the
   // MFMAs in the log2 domain.
-  const float c = a.qk_scale_log2;
+  // (Loaded in the prologue, after the first copies are issued, so that the
+  // two memory latencies overlap.)
   bf16x8 qf[QB][DT];
+  auto load_q = [&]() {
+    const float c = a.qk_scale_log2;
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const int pos = min(wp0 + 32 * qb + lq, a.S - 1);
-    if (a.qb) {  // already scaled and rounded (the fused prefill step)
-      const bf16 *qp = a.qb + ((long)pos * a.Hq + head) * D + 8 * hl;
+    for (int qb = 0; qb < QB; ++qb) {
+      const int pos = min(wp0 + 32 * qb + lq, a.S - 1);
+      if (a.qb) {  // already scaled and rounded (the fused prefill step)
+        const bf16 *qp = a.qb + ((long)pos * a.Hq + head) * D + 8 * hl;
 #pragma unroll
-      for (int t = 0; t < DT; ++t) qf[qb][t] = *reinterpret_cast<const bf16x8 *>(qp + 16 * t);
-      continue;
+        for (int t = 0; t < DT; ++t) qf[qb][t] = *reinterpret_cast<const bf16x8 *>(qp + 16 * t);
+        continue;
+      }
+      const float *qp = a.q + ((long)pos * a.Hq + head) * D + 8 * hl;
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+        const float4 x0 = *reinterpret_cast<const float4 *>(qp + 16 * t);
+        const float4 x1 = *reinterpret_cast<const float4 *>(qp + 16 * t + 4);
+        bf16x8 v;
+        v[0] = (bf16)(x0.x * c); v[1] = (bf16)(x0.y * c); v[2] = (bf16)(x0.z * c); v[3] = (bf16)(x0.w * c);
+        v[4] = (bf16)(x1.x * c); v[5] = (bf16)(x1.y * c); v[6] = (bf16)(x1.z * c); v[7] = (bf16)(x1.w * c);
+        qf[qb][t] = v;
+      }
     }
-    const float *qp = a.q + ((long)pos * a.Hq + head) * D + 8 * hl;
-#pragma unroll
-    for (int t = 0; t < DT; ++t) {
-      const float4 x0 = *reinterpret_cast<const float4 *>(qp + 16 * t);
-      const float4 x1 = *reinterpret_cast<const float4 *>(qp + 16 * t + 4);
-      bf16x8 v;
-      v[0] = (bf16)(x0.x * c); v[1] = (bf16)(x0.y * c); v[2] = (bf16)(x0.z * c); v[3] = (bf16)(x0.w * c);
-      v[4] = (bf16)(x1.x * c); v[5] = (bf16)(x1.y * c); v[6] = (bf16)(x1.z * c); v[7] = (bf16)(x1.w * c);
-      qf[qb][t] = v;
-    }
-  }
+  };
   f32x16 oacc[QB][DB];
   float m[QB], l[QB];
 #pragma unroll
@@ -576,6 +580,7 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
   copy_k(t_begin, k_lds0);
   copy_v(t_begin, v_lds0);
   if (t_begin + 1 < t_end) copy_k(t_begin + 1, k_lds1);
+  load_q();
   wait_copies();
   copies_barrier();
 #pragma unroll
