@@ -308,56 +308,7 @@ def gpu_bench(args) -> dict:
 
         # ---- causal prefill, 4096 tokens, no cache ----
         if not args.decode_only:
-            log("timing prefill")
-            pq = [torch.randn(PREFILL_S * HQ * D, generator=gen, device=dev) for _ in range(LAYERS)]
-            pk = [torch.randn(PREFILL_S * w, generator=gen, device=dev) for _ in range(LAYERS)]
-            pv = [torch.randn(PREFILL_S * w, generator=gen, device=dev) for _ in range(LAYERS)]
-            po = [torch.empty(PREFILL_S * HQ * D, device=dev) for _ in range(LAYERS)]
-            cfgp = KvAttentionConfig(PREFILL_S, HQ, HKV, D, True)
-
-            ptable = sess.rope_table(_ffi.ROPE_LLAMA, D, THETA, max_positions=PREFILL_S + 64)
-            pcaches = [sess.kv_cache(HKV, D, PREFILL_S) for _ in range(LAYERS)]
-
-            def call_order():
-                # the reference's attention call: f32 K/V of the prompt passed in
-                # (converted to the bf16 operands inside the call), no cache
-                for l in range(LAYERS):
-                    sess.attention(pq[l], pk[l], pv[l], None, cfgp, po[l])
-
-            def fused_step():
-                # RoPE + append (f32 rows and bf16 operands) + staged q, then attention
-                for l in range(LAYERS):
-                    sess.prefill_step(ptable, pq[l], pk[l], pv[l], pcaches[l], cfgp, po[l])
-
-            def attention_phase():
-                # the step's attention launch alone: the prompt is already in the cache
-                for l in range(LAYERS):
-                    sess.attention_cached(pq[l], pcaches[l], cfgp, po[l])
-
-            call_order()
-            fused_step()
-            sess.sync()
-            for c in pcaches:
-                c.truncate(0)
-            graphs = {}
-            for name, fn in (("call", call_order), ("step", fused_step), ("attn", attention_phase)):
-                graphs[name] = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(graphs[name], stream=stream):
-                    fn()  # the step's capture appends the prompt, so the attention phase sees it
-            fl = prefill_flops(PREFILL_S)
-            ms = {name: time_graph(g, max(3, args.steps // 4), 2) for name, g in graphs.items()}
-
-            def rec(m):
-                return {"ms_per_step": m, "us_per_layer": m * 1e3 / LAYERS,
-                        "TFLOPs": LAYERS * fl / (m * 1e-3) / 1e12, "tokens_per_s": PREFILL_S * 1e3 / m,
-                        "flop_per_layer": fl}
-
-            res["prefill_4096"] = rec(ms["attn"])
-            res["prefill_step_4096"] = rec(ms["step"])
-            res["prefill_step_4096"]["rope_append_us_per_layer"] = (ms["step"] - ms["attn"]) * 1e3 / LAYERS
-            res["prefill_call_4096"] = rec(ms["call"])
-            del graphs, pq, pk, pv, po, pcaches
-            torch.cuda.empty_cache()
+            res.update(prefill_bench(sess, stream, gen, dev, args, time_graph))
 
         # ---- the projections either side (q/k/v fused, bf16 weights) ----
         if not args.decode_only:
@@ -894,6 +845,71 @@ def configs_bench(sess, stream, gen, dev, args, time_graph) -> dict:
     return out
 
 
+def prefill_bench(sess, stream, gen, dev, args, time_graph) -> dict:
+    """The 4096-token causal prefill of config 2a over 28 layers: the attention
+    call in the reference's order, the fused prefill step, and the step's
+    attention launch alone (records prefill_call_4096, prefill_step_4096,
+    prefill_4096)."""
+    import torch
+
+    from spissa_amd import _ffi
+    from spissa_amd.rotary import KvAttentionConfig
+
+    res = {}
+    w = HKV * D
+    log("timing prefill")
+    pq = [torch.randn(PREFILL_S * HQ * D, generator=gen, device=dev) for _ in range(LAYERS)]
+    pk = [torch.randn(PREFILL_S * w, generator=gen, device=dev) for _ in range(LAYERS)]
+    pv = [torch.randn(PREFILL_S * w, generator=gen, device=dev) for _ in range(LAYERS)]
+    po = [torch.empty(PREFILL_S * HQ * D, device=dev) for _ in range(LAYERS)]
+    cfgp = KvAttentionConfig(PREFILL_S, HQ, HKV, D, True)
+
+    ptable = sess.rope_table(_ffi.ROPE_LLAMA, D, THETA, max_positions=PREFILL_S + 64)
+    pcaches = [sess.kv_cache(HKV, D, PREFILL_S) for _ in range(LAYERS)]
+
+    def call_order():
+        # the reference's attention call: f32 K/V of the prompt passed in
+        # (converted to the bf16 operands inside the call), no cache
+        for l in range(LAYERS):
+            sess.attention(pq[l], pk[l], pv[l], None, cfgp, po[l])
+
+    def fused_step():
+        # RoPE + append (f32 rows and bf16 operands) + staged q, then attention
+        for l in range(LAYERS):
+            sess.prefill_step(ptable, pq[l], pk[l], pv[l], pcaches[l], cfgp, po[l])
+
+    def attention_phase():
+        # the step's attention launch alone: the prompt is already in the cache
+        for l in range(LAYERS):
+            sess.attention_cached(pq[l], pcaches[l], cfgp, po[l])
+
+    call_order()
+    fused_step()
+    sess.sync()
+    for c in pcaches:
+        c.truncate(0)
+    graphs = {}
+    for name, fn in (("call", call_order), ("step", fused_step), ("attn", attention_phase)):
+        graphs[name] = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graphs[name], stream=stream):
+            fn()  # the step's capture appends the prompt, so the attention phase sees it
+    fl = prefill_flops(PREFILL_S)
+    ms = {name: time_graph(g, max(3, args.steps // 4), 2) for name, g in graphs.items()}
+
+    def rec(m):
+        return {"ms_per_step": m, "us_per_layer": m * 1e3 / LAYERS,
+                "TFLOPs": LAYERS * fl / (m * 1e-3) / 1e12, "tokens_per_s": PREFILL_S * 1e3 / m,
+                "flop_per_layer": fl}
+
+    res["prefill_4096"] = rec(ms["attn"])
+    res["prefill_step_4096"] = rec(ms["step"])
+    res["prefill_step_4096"]["rope_append_us_per_layer"] = (ms["step"] - ms["attn"]) * 1e3 / LAYERS
+    res["prefill_call_4096"] = rec(ms["call"])
+    del graphs, pq, pk, pv, po, pcaches
+    torch.cuda.empty_cache()
+    return res
+
+
 def configs_only(args) -> dict:
     """The records of the CONFIG_CASES named in --configs, nothing else."""
     import torch
@@ -919,9 +935,13 @@ def configs_only(args) -> dict:
         sess.sync()
         return a.elapsed_time(b) / reps
 
-    out = configs_bench(sess, stream, gen, dev, args, time_graph)
-    if "projections" in args.configs.split(","):
-        out["projections"] = projection_bench(sess, stream, gen, dev, args, time_graph)
+    names = args.configs.split(",")
+    with torch.cuda.stream(stream):
+        out = configs_bench(sess, stream, gen, dev, args, time_graph)
+        if "projections" in names:
+            out["projections"] = projection_bench(sess, stream, gen, dev, args, time_graph)
+        if "prefill_4096" in names:
+            out.update(prefill_bench(sess, stream, gen, dev, args, time_graph))
     return out
 
 
@@ -1081,8 +1101,8 @@ def main() -> int:
                     help="also run a 256 MiB device copy (HBM-counter calibration under rocprofv3 --pmc)")
     ap.add_argument("--configs", default="",
                     help="only time these comma-separated cases of CONFIG_CASES (and 'projections': the "
-                         "q/k/v projection at batch 1, 16 and 4096) and print their records (for counter "
-                         "passes); the benchmark line is not printed")
+                         "q/k/v projection at batch 1, 16 and 4096; 'prefill_4096': config 2a's prefill) and "
+                         "print their records (for counter passes); the benchmark line is not printed")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build's attention path has no multi-GPU leg "
