@@ -271,7 +271,8 @@ typedef struct {
     int tile_keys;          /* prefill: keys per tile */
     int workgroup_queries;  /* prefill: queries per workgroup */
     int o_split;            /* always 0 (no kernel splits O over waves; kept for the struct's layout) */
-    int xcd_group;          /* prefill with key splits: the workgroups of one KV head's split share an XCD */
+    int xcd_group;          /* prefill: 1 = with key splits, the workgroups of one KV head's split share an XCD;
+                               2 = unsplit windowed, each XCD takes a contiguous run of query blocks */
     long max_tiles;         /* prefill: most key tiles one unsplit workgroup visits */
     size_t workgroups;      /* attention kernel grid (decode: its first launch of <= 16 sequences) */
     size_t partial_bytes;   /* decode: split partials of the largest launch; prefill: key-split partials */

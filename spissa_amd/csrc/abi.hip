@@ -1149,7 +1149,7 @@ static void plan_prefill(PrefillArgs &a, int D, int cus, PrefillPlan *p) {
     a.tps = 0;
     p->ppart_bytes = 0;
   }
-  a.xcd_group = prefill_use_xcd_group(a, D) ? 1 : 0;
+  a.xcd_group = prefill_use_xcd_group(a, D);
   const int wgq = prefill_wg_queries(a, D);
   p->workgroups = (size_t)prefill_grid_workgroups((S + wgq - 1) / wgq, a.R / prefill_wg_heads(a, D), a.Hkv, a.splits,
                                                   a.xcd_group);

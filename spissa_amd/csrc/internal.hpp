@@ -119,10 +119,12 @@ struct PrefillArgs {
   // key); launch_prefill_combine merges them. splits == 1 writes `out`.
   int splits, tps;
   float *part_o, *part_ml;
-  // With key splits: the workgroups that read one KV head's split (its head
-  // blocks and query blocks) are given ids 8 apart, so they run on one XCD
-  // and share its L2 (prefill_use_xcd_group decides; the grid is padded to a
-  // multiple of 8 units).
+  // 1 (with key splits): the workgroups that read one KV head's split (its
+  // head blocks and query blocks) are given ids 8 apart, so they run on one
+  // XCD and share its L2 (the grid is padded to a multiple of 8 units).
+  // 2 (unsplit windowed layers): the ids of one XCD take a contiguous run of
+  // the workgroup order (the grid is padded to a multiple of 8).
+  // prefill_use_xcd_group decides.
   int xcd_group;
 };
 
@@ -139,7 +141,7 @@ long prefill_max_tile_span(const PrefillArgs &a, int D);
 // Workgroups of a prefill launch of n_qblocks x head_blocks x Hkv x splits
 // (grouped by XCD: units of one KV head and split padded to a multiple of 8).
 long prefill_grid_workgroups(long n_qblocks, long head_blocks, long Hkv, long splits, int xcd_group);
-bool prefill_use_xcd_group(const PrefillArgs &a, int D);
+int prefill_use_xcd_group(const PrefillArgs &a, int D);
 
 struct GenericArgs {
   const float *q;  // [S, Hq, D]

@@ -225,7 +225,7 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
 
   const int HB = a.R / RB;
   int h, hb, split, qt;
-  if (a.xcd_group) {
+  if (a.xcd_group == 1) {
     // Workgroup ids 8 apart run on one XCD. The HB * n_qblocks workgroups
     // that read the same keys (one KV head, one split) get ids
     // lo + 8 * (g + G * hi), unit = 8 * hi + lo, so that they share that
@@ -240,6 +240,10 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
     qt = a.n_qblocks - 1 - g / HB;
   } else {
     int bid = blockIdx.x;
+    if (a.xcd_group == 2) {  // ids of one XCD (equal mod 8) take a contiguous run
+      bid = (int)(blockIdx.x & 7) * (int)(gridDim.x >> 3) + (int)(blockIdx.x >> 3);
+      if (bid >= a.n_qblocks * HB * a.Hkv * a.splits) return;  // padding to a multiple of 8
+    }
     const int hh = bid % (a.Hkv * HB);
     bid /= (a.Hkv * HB);
     split = bid % a.splits;
@@ -743,7 +747,7 @@ __global__ __launch_bounds__(RB *NPB * 64, NST > 2 ? 1 : 2) void prefill_q16_ker
 
   const int HB = a.R / RB;
   int h, hb, split, qt;
-  if (a.xcd_group) {
+  if (a.xcd_group == 1) {
     const int Gq = HB * a.n_qblocks;
     const int lo = (int)(blockIdx.x & 7), rest = (int)(blockIdx.x >> 3);
     const int gg = rest % Gq, unit = (rest / Gq) * 8 + lo;
@@ -754,6 +758,10 @@ __global__ __launch_bounds__(RB *NPB * 64, NST > 2 ? 1 : 2) void prefill_q16_ker
     qt = a.n_qblocks - 1 - gg / HB;
   } else {
     int bid = blockIdx.x;
+    if (a.xcd_group == 2) {
+      bid = (int)(blockIdx.x & 7) * (int)(gridDim.x >> 3) + (int)(blockIdx.x >> 3);
+      if (bid >= a.n_qblocks * HB * a.Hkv * a.splits) return;
+    }
     const int hh = bid % (a.Hkv * HB);
     bid /= (a.Hkv * HB);
     split = bid % a.splits;
@@ -1183,15 +1191,22 @@ long prefill_base_workgroups(const PrefillArgs &a, int D) {
 }
 
 long prefill_grid_workgroups(long n_qblocks, long head_blocks, long Hkv, long splits, int xcd_group) {
-  if (!xcd_group) return n_qblocks * head_blocks * Hkv * splits;
+  const long n = n_qblocks * head_blocks * Hkv * splits;
+  if (xcd_group == 2) return (n + 7) / 8 * 8;
+  if (!xcd_group) return n;
   const long units = (Hkv * splits + 7) / 8 * 8;
   return units * head_blocks * n_qblocks;
 }
 
-bool prefill_use_xcd_group(const PrefillArgs &a, int D) {
+int prefill_use_xcd_group(const PrefillArgs &a, int D) {
   const int wgq = prefill_wg_queries(a, D);
   const long G = (long)(a.R / prefill_wg_heads(a, D)) * ((a.S + wgq - 1) / wgq);
-  return a.splits > 1 && (long)a.Hkv * a.splits >= 8 && G > 1;
+  if (a.splits > 1 && (long)a.Hkv * a.splits >= 8 && G > 1) return 1;
+  // Unsplit windowed layers of at least two workgroups per XCD: a contiguous
+  // run of query blocks per XCD, whose windows overlap in that XCD's L2
+  // (round-robin ids make every XCD fetch nearly all of the keys).
+  if (a.splits == 1 && a.window > 0 && G * a.Hkv >= 16) return 2;
+  return 0;
 }
 
 // The largest t_end - t_begin of prefill_kernel over its query blocks, with

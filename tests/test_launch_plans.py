@@ -78,19 +78,35 @@ def check_decode(cfg, past, plan, noalloc=False):
 
 def check_prefill_grid(plan, n_qblocks, Hkv, HB, splits):
     """prefill_kernel's workgroup id -> (KV head, head block, split, query
-    block) decode: every tuple exactly once; with xcd_group, the workgroups of
-    one (KV head, split) have ids equal mod 8 (one XCD) and the padding ids
-    decode to units past the last."""
+    block) decode: every tuple exactly once; with xcd_group 1, the workgroups
+    of one (KV head, split) have ids equal mod 8 (one XCD) and the padding ids
+    decode to units past the last; with xcd_group 2, each XCD's ids take a
+    contiguous run of the unsplit order (query blocks adjacent) and the
+    padding ids decode past its end."""
     G = HB * n_qblocks
     units = Hkv * splits
     seen, xcd = set(), {}
-    if plan["xcd_group"]:
+    n = units * G
+    if plan["xcd_group"] == 1:
         assert splits > 1 and units >= 8 and G > 1
         assert plan["workgroups"] == -(-units // 8) * 8 * G
+    elif plan["xcd_group"] == 2:
+        assert splits == 1 and n >= 16
+        assert plan["workgroups"] == -(-n // 8) * 8
     else:
-        assert plan["workgroups"] == units * G
+        assert plan["workgroups"] == n
+    runs = {}
     for bid in range(plan["workgroups"]):
-        if plan["xcd_group"]:
+        if plan["xcd_group"] == 2:
+            r = (bid & 7) * (plan["workgroups"] >> 3) + (bid >> 3)
+            if r >= n:
+                continue
+            runs.setdefault(bid & 7, []).append(r)
+            hh = r % (Hkv * HB)
+            r //= Hkv * HB
+            split, qt = r % splits, n_qblocks - 1 - r // splits
+            h, hb = hh // HB, hh % HB
+        elif plan["xcd_group"] == 1:
             lo, rest = bid & 7, bid >> 3
             g, unit = rest % G, (rest // G) * 8 + lo
             if unit >= units:
@@ -108,8 +124,11 @@ def check_prefill_grid(plan, n_qblocks, Hkv, HB, splits):
         seen.add(key)
         xcd.setdefault((h, split), set()).add(bid % 8)
     assert len(seen) == units * G
-    if plan["xcd_group"]:
+    if plan["xcd_group"] == 1:
         assert all(len(v) == 1 for v in xcd.values())
+    if plan["xcd_group"] == 2:
+        for ids in runs.values():
+            assert ids == list(range(ids[0], ids[0] + len(ids)))
 
 
 def check_prefill(cfg, P, plan):
@@ -248,6 +267,9 @@ def test_split_prefill_groups_shared_keys_on_one_xcd():
     assert plan["splits"] > 1 and plan["xcd_group"] == 1
     # unsplit prefill keeps the longest-first order
     assert plan_attention(KvAttentionConfig(4096, 24, 8, 128, True, 0), [0])["xcd_group"] == 0
+    # Gemma-3-1B local W512 (one KV head, unsplit): adjacent query blocks per XCD
+    plan = plan_attention(KvAttentionConfig(4096, 4, 1, 256, True, 512), [0])
+    assert plan["splits"] == 1 and plan["xcd_group"] == 2
 
 
 def test_prefill_plan_sweep():
