@@ -13,7 +13,7 @@ bytes: each KV head's visible K/V rows once, q/out, append); extra fields give
 `roofline` of the dominant decode kernel (event-timed back-to-back launches),
 and `cpu_baseline` (the oracle on this host's cores over a bounded sample).
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--decode-only]
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--decode-only] [--skip-workloads]
 """
 from __future__ import annotations
 
@@ -48,15 +48,43 @@ def prefill_flops(s: int, hq=HQ, d=D) -> float:
 TRAFFIC_PROFILE = ROOT / "profiles" / "decode_b1_hbm_traffic.md"
 
 
-def measured_traffic():
-    """HBM bytes per decode launch from the committed calibrated counter summary."""
+# Plan fields a traffic profile records for the launch it measured.
+TRAFFIC_PLAN_FIELDS = ("heads_per_block", "head_blocks", "keys_per_split", "splits", "token_split", "workgroups")
+
+
+def decode_plan() -> dict:
+    """The launch geometry of the batch-1 decode at 8192 cached keys, as the
+    library plans it (spissa_plan_attention, host arithmetic only)."""
+    from spissa_amd.device import plan_attention
+    from spissa_amd.rotary import KvAttentionConfig
+
+    plan = plan_attention(KvAttentionConfig(1, HQ, HKV, D, True), [CTX])
+    return {k: plan[k] for k in TRAFFIC_PLAN_FIELDS}
+
+
+def measured_traffic(plan=None) -> dict:
+    """HBM bytes per decode launch from the committed calibrated counter
+    summary, with the plan it was measured on. The bytes are withheld (None)
+    when that plan differs from the launch the library plans now: the counts
+    would belong to kernels that no longer run."""
+    out = {"bytes": None, "profile_plan": None, "stale": None}
     try:
-        for line in TRAFFIC_PROFILE.read_text().splitlines():
-            if line.startswith("traffic_bytes_per_launch:"):
-                return int(line.split(":", 1)[1])
+        text = TRAFFIC_PROFILE.read_text()
     except OSError:
-        pass
-    return None
+        return out
+    nbytes, recorded = None, {}
+    for line in text.splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            nbytes = int(line.split(":", 1)[1])
+        elif line.startswith("plan:"):
+            for item in line.split(":", 1)[1].split():
+                k, _, v = item.partition("=")
+                recorded[k] = int(v)
+    out["profile_plan"] = recorded or None
+    if plan is not None:
+        out["stale"] = recorded != plan
+    out["bytes"] = nbytes if (plan is None or not out["stale"]) else None
+    return out
 
 
 def log(msg: str) -> None:
@@ -318,8 +346,9 @@ def gpu_bench(args) -> dict:
             res["lm_head"] = lm_head_bench(sess, stream, gen, dev, args, time_graph)
             log("timing the other BASELINE configs")
             res["configs"] = configs_bench(sess, stream, gen, dev, args, time_graph)
-            log("timing the Gemma workloads")
-            res["workloads"] = workloads_bench(sess, stream, gen, dev, args, time_graph)
+            if not args.skip_workloads:
+                log("timing the Gemma workloads")
+                res["workloads"] = workloads_bench(sess, stream, gen, dev, args, time_graph)
     return res
 
 
@@ -498,6 +527,8 @@ CONFIG_CASES = [
 
 # Gemma 3 layer schedule (models/gemma/model.rs:46-51): global iff (layer + 1) % 6 == 0.
 GEMMA_PATTERN = 6
+# Decode tokens per captured graph of the Gemma-3-4B turn.
+TURN_GRAPH_TOKENS = 16
 GEMMA_WORKLOADS = {  # BASELINE configs 3 and 4: heads, head_dim, layers, local window
     "gemma3_1b": {"config": 3, "hq": 4, "hkv": 1, "d": 256, "layers": 26, "window": 512},
     "gemma3_4b": {"config": 4, "hq": 8, "hkv": 4, "d": 256, "layers": 34, "window": 1024},
@@ -704,19 +735,21 @@ def workloads_bench(sess, stream, gen, dev, args, time_graph) -> dict:
             sess.gemma_qk_prologue(tab[kinds[l]], q[l], k[l], 1, hq, hkv, d, qn[l], kn[l], 1e-6, pos, 1.0)
             sess.decode_step(None, q[l], k[l], v[l], [caches[l]], dcfg[l], o[l])
 
-    def turn():
-        chunk()
-        for _ in range(T):
-            decode_token()
-
     def reset():
         for c in caches:
             c.truncate(P)
 
-    turn()  # sizes every workspace and creates the caches' bf16 operands
+    chunk()  # sizes every workspace and creates the caches' bf16 operands
+    for _ in range(T):
+        decode_token()
     sess.sync()
     reset()
-    g_turn = captured(turn)
+    # The turn as one graph for the chunk and one per TURN_GRAPH_TOKENS decode
+    # tokens (each token's launches carry its own cache position), replayed back
+    # to back: no graph holds more than 16 x 34 x 2 = 1088 dispatches.
+    g_turn = [captured(chunk)]
+    for _ in range(T // TURN_GRAPH_TOKENS):
+        g_turn.append(captured(lambda: [decode_token() for _ in range(TURN_GRAPH_TOKENS)]))
     reset()
     g_chunk = captured(chunk)  # then one decode token right after the chunk, with its phases
     g_tok = captured(decode_token)
@@ -737,7 +770,8 @@ def workloads_bench(sess, stream, gen, dev, args, time_graph) -> dict:
     g_tok_rot = captured(tok_prologue)
     g_tok_step = captured(tok_steps)
     reset()
-    ms_turn = time_graph(g_turn, 3, 1)
+    ms_turn = time_graphs(g_turn, 3, 1)
+    sess.sync()
     ms_chunk = time_graph(g_chunk, reps, 2)
     ms_tok = time_graph(g_tok, max(5, args.steps), 3)
     ms_unf = time_graph(g_tok_unf, max(5, args.steps), 3)
@@ -758,6 +792,25 @@ def workloads_bench(sess, stream, gen, dev, args, time_graph) -> dict:
     del g_turn, g_chunk, g_tok, g_tok_unf, g_tok_rot, g_tok_step, caches
     torch.cuda.empty_cache()
     return out
+
+
+def time_graphs(graphs, reps, warm) -> float:
+    """ms per replay of a sequence of graphs launched back to back on the
+    current stream (event-timed around reps sequences)."""
+    import torch
+
+    for _ in range(warm):
+        for g in graphs:
+            g.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        for g in graphs:
+            g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / reps
 
 
 def visible_pairs(S: int, P: int, window: int) -> int:
@@ -846,10 +899,13 @@ def configs_bench(sess, stream, gen, dev, args, time_graph) -> dict:
 
 
 def prefill_bench(sess, stream, gen, dev, args, time_graph) -> dict:
-    """The 4096-token causal prefill of config 2a over 28 layers: the attention
-    call in the reference's order, the fused prefill step, and the step's
-    attention launch alone (records prefill_call_4096, prefill_step_4096,
-    prefill_4096)."""
+    """The 4096-token causal prefill of config 2a over 28 layers, three forms:
+    prefill_4096 = the attention call in the reference's order (the prompt's
+    f32 q/k/v passed in, no cache; the bf16 K/V operands are made inside the
+    call, rotary.rs:335-415); prefill_step_4096 = the fused prefill step (RoPE,
+    append of the f32 rows and bf16 operands, staged q, then attention);
+    prefill_attention_4096 = the step's attention launch alone over a cache
+    that already holds the prompt (the dominant kernel's MFMA rate)."""
     import torch
 
     from spissa_amd import _ffi
@@ -901,10 +957,10 @@ def prefill_bench(sess, stream, gen, dev, args, time_graph) -> dict:
                 "TFLOPs": LAYERS * fl / (m * 1e-3) / 1e12, "tokens_per_s": PREFILL_S * 1e3 / m,
                 "flop_per_layer": fl}
 
-    res["prefill_4096"] = rec(ms["attn"])
+    res["prefill_4096"] = rec(ms["call"])
     res["prefill_step_4096"] = rec(ms["step"])
     res["prefill_step_4096"]["rope_append_us_per_layer"] = (ms["step"] - ms["attn"]) * 1e3 / LAYERS
-    res["prefill_call_4096"] = rec(ms["call"])
+    res["prefill_attention_4096"] = rec(ms["attn"])
     del graphs, pq, pk, pv, po, pcaches
     torch.cuda.empty_cache()
     return res
@@ -1090,6 +1146,45 @@ def cpu_baseline(args) -> dict:
     return out
 
 
+def headline(res: dict, cpu) -> dict:
+    """The figures the north star names, compactly, for the end of the line."""
+    def r(v, n=3):
+        return None if v is None else round(v, n)
+
+    d1 = res["decode_b1"]
+    h = {"decode_b1_us_per_layer": r(d1["us_per_layer"]), "decode_b1_GBps": r(d1["GBps"], 1),
+         "decode_b1_hbm_frac": r(d1["GBps"] / HBM_PEAK_GBS, 4),
+         "decode_b1_attn_kernel_us": r(d1["attn_kernel_us"]),
+         "decode_b1_attn_kernel_hbm_frac": r(d1["attn_kernel_GBps"] / HBM_PEAK_GBS, 4)}
+    if "decode_b16" in res:
+        b = res["decode_b16"]
+        h.update(decode_b16_us_per_layer=r(b["us_per_layer"]), decode_b16_hbm_frac=r(b["GBps"] / HBM_PEAK_GBS, 4))
+    for key, short in (("prefill_4096", "prefill_call"), ("prefill_step_4096", "prefill_step"),
+                       ("prefill_attention_4096", "prefill_attention")):
+        if key in res:
+            p = res[key]
+            h[f"{short}_us_per_layer"] = r(p["us_per_layer"])
+            h[f"{short}_TFLOPs"] = r(p["TFLOPs"], 1)
+            h[f"{short}_mfma_frac"] = r(p["TFLOPs"] / BF16_PEAK_TFLOPS, 4)
+    ceil = res.get("hbm_read_ceiling") or {}
+    if "layer_67MB" in ceil:
+        h["hbm_read_ceiling_GBps"] = ceil["layer_67MB"]["GBps"]
+    if res.get("mfma_ceiling"):
+        h["mfma_ceiling_TFLOPs"] = res["mfma_ceiling"]["TFLOPs"]
+    wl = res.get("workloads") or {}
+    if "gemma3_1b" in wl:
+        h["gemma3_1b_prefill_4096_ms"] = wl["gemma3_1b"]["prefill_4096"]["ms"]
+        h["gemma3_1b_decode_32768_ms_per_token"] = wl["gemma3_1b"]["decode_32768"]["ms_per_token"]
+    if "gemma3_4b" in wl:
+        h["gemma3_4b_turn_ms"] = wl["gemma3_4b"]["turn"]["ms"]
+        h["gemma3_4b_decode_token_ms"] = wl["gemma3_4b"]["decode_token_after_chunk"]["ms"]
+    if cpu is not None:
+        h["cpu_decode_b1_us_per_layer"] = cpu["us_per_layer"]
+        if "prefill" in cpu:
+            h["cpu_prefill_4096_us_per_layer"] = round(cpu["prefill"]["us_per_layer"], 1)
+    return h
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -1097,6 +1192,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-only", action="store_true")
+    ap.add_argument("--skip-workloads", action="store_true",
+                    help="leave out the Gemma workloads (for counter passes: three whole-bench rocprofv3 --pmc "
+                         "runs ended in a SIGSEGV in the profiler's threads while these graphs replayed)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a 256 MiB device copy (HBM-counter calibration under rocprofv3 --pmc)")
     ap.add_argument("--configs", default="",
@@ -1117,6 +1215,8 @@ def main() -> int:
     log(f"gpu part done in {time.time() - t0:.1f}s")
     cpu = None if args.no_cpu else cpu_baseline(args)
     d1 = res["decode_b1"]
+    plan = decode_plan()
+    traffic = measured_traffic(plan)
     line = {
         "metric": "decode-attn HBM GB/s + us/layer; prefill-attn TFLOP/s (Llama-3.2-3B shape)",
         "value": round(d1["GBps"], 1),
@@ -1134,42 +1234,25 @@ def main() -> int:
                                "(RoPE + split-K decode + KV append per layer, fused in two launches)",
                    "heads": f"{HQ}q/{HKV}kv", "head_dim": D, "context": CTX, "layers": LAYERS},
         "us_per_layer": round(d1["us_per_layer"], 3),
-        "decode_b1": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in d1.items()},
         "roofline": {
             "bound": "hbm",
             "achieved": round(d1["attn_kernel_GBps"], 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(d1["attn_kernel_GBps"] / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(),
+            "traffic": traffic["bytes"],
             "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, calibrated on copies of known size "
-                              "(profiles/decode_b1_hbm_traffic.md)",
+                              "(profiles/decode_b1_hbm_traffic.md), withheld when the profile's plan differs "
+                              "from the current launch",
+            "traffic_plan": traffic["profile_plan"],
+            "plan": plan,
             "kernel": "one decode attention launch = decode_split_kernel<128,3,3> + decode_combine_kernel<128,3>; "
                       "event-timed average over 28 back-to-back launches per graph replay",
         },
-        "hbm_read_ceiling": res.get("hbm_read_ceiling"),
-        "mfma_ceiling": res.get("mfma_ceiling"),
         "device": res.get("device"),
     }
-    if "decode_b16" in res:
-        line["decode_b16"] = {k: round(v, 3) for k, v in res["decode_b16"].items()}
-    if "prefill_4096" in res:
-        p = res["prefill_4096"]
-        line["prefill_4096"] = {"phase": "attention (the prompt's K/V already appended to the layer's cache, "
-                                         "as the fused prefill step's second launch)",
-                                **{k: round(v, 3) for k, v in p.items()}}
-        line["prefill_step_4096"] = {"phase": "fused prefill step: RoPE + append of f32 rows and bf16 operands "
-                                              "+ staged q, then attention",
-                                     **{k: round(v, 3) for k, v in res["prefill_step_4096"].items()}}
-        line["prefill_call_4096"] = {"phase": "the attention call in the reference's order (f32 K/V of the "
-                                              "prompt converted inside the call, no cache)",
-                                     **{k: round(v, 3) for k, v in res["prefill_call_4096"].items()}}
-        line["roofline_prefill"] = {"bound": "mfma", "achieved": round(p["TFLOPs"], 2), "peak": BF16_PEAK_TFLOPS,
-                                    "unit": "TFLOP/s", "frac": round(p["TFLOPs"] / BF16_PEAK_TFLOPS, 4),
-                                    "dtype": "bf16 MFMA, f32 accumulate"}
-        if res.get("mfma_ceiling"):
-            line["roofline_prefill"]["frac_of_measured_ceiling"] = round(
-                p["TFLOPs"] / res["mfma_ceiling"]["TFLOPs"], 4)
+    # Detail blocks first; the headline figures close the line (its tail is
+    # what a log keeps).
     if "sublayer_b1" in res:
         line["sublayer_b1"] = {"workload": "llama-3.2-3B attention sublayer at decode, batch 1, 8192-token "
                                            "cache: input RMSNorm, q/k/v projections (bf16), RoPE + attention "
@@ -1199,6 +1282,32 @@ def main() -> int:
                              **res["workloads"]}
     if cpu is not None:
         line["cpu_baseline"] = cpu
+    line["hbm_read_ceiling"] = res.get("hbm_read_ceiling")
+    line["mfma_ceiling"] = res.get("mfma_ceiling")
+    line["decode_b1"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in d1.items()}
+    if "decode_b16" in res:
+        line["decode_b16"] = {k: round(v, 3) for k, v in res["decode_b16"].items()}
+    phases = {
+        "prefill_4096": "the attention call in the reference's order (f32 q/k/v of the prompt, no cache; the "
+                        "bf16 K/V operands are made inside the call)",
+        "prefill_step_4096": "fused prefill step: RoPE + append of f32 rows and bf16 operands + staged q, then "
+                             "attention",
+        "prefill_attention_4096": "the fused step's attention launch alone (the prompt already in the cache)",
+    }
+    for key, phase in phases.items():
+        if key in res:
+            line[key] = {"phase": phase, **{k: round(v, 3) for k, v in res[key].items()}}
+    if "prefill_attention_4096" in res:
+        p = res["prefill_attention_4096"]
+        line["roofline_prefill"] = {"bound": "mfma", "kernel": "prefill_kernel<128,1,4,64,1> (the attention "
+                                                                "launch of prefill_attention_4096)",
+                                    "achieved": round(p["TFLOPs"], 2), "peak": BF16_PEAK_TFLOPS,
+                                    "unit": "TFLOP/s", "frac": round(p["TFLOPs"] / BF16_PEAK_TFLOPS, 4),
+                                    "dtype": "bf16 MFMA, f32 accumulate"}
+        if res.get("mfma_ceiling"):
+            line["roofline_prefill"]["frac_of_measured_ceiling"] = round(
+                p["TFLOPs"] / res["mfma_ceiling"]["TFLOPs"], 4)
+    line["headline"] = headline(res, cpu)
     print(json.dumps(line), flush=True)
     return 0
 

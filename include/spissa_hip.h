@@ -266,7 +266,8 @@ typedef struct {
     int head_blocks;        /* head blocks per KV head */
     int keys_per_split;     /* decode: cached keys per split workgroup */
     int splits;             /* decode: splits of the longest sequence, the token's own included; prefill: key splits (1: none) */
-    int token_split;        /* decode: the new token has a split of its own after the cached keys' (else split 0 takes it) */
+    int token_split;        /* decode: 1 = split 0 is the new token's own split, dispatched first, and the cached
+                               keys' splits are 1..splits-1; 0 = cached split 0 takes the token after its rows */
     int tiles_per_split;    /* prefill with key splits: key tiles per split */
     int tile_keys;          /* prefill: keys per tile */
     int workgroup_queries;  /* prefill: queries per workgroup */

@@ -73,9 +73,10 @@ struct DecodeArgs {
   int window;
   int kps;             // cached keys per split
   int max_splits;      // splits of the longest sequence in the launch (with the token's own)
-  // 1: the new token is a split of its own after the cached keys' (its
-  // latency -- loads, QK-norm, RoPE, append -- then overlaps the streaming
-  // splits); 0: split 0 takes it after its cached rows.
+  // 1: split 0 is the new token's own split, dispatched first, and the cached
+  // keys' splits are 1..max_splits-1 (the token's latency -- loads, QK-norm,
+  // RoPE, append -- then overlaps the streaming splits); 0: cached split 0
+  // takes the token after its cached rows.
   int tok_split;
   float qscale;        // softmax scale * log2(e), applied to the scores
   SeqDesc seq[kMaxDecodeBatch];

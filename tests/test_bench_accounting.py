@@ -36,3 +36,21 @@ def test_config_cases_cover_every_other_baseline_config():
     assert {c[1] for c in bench.CONFIG_CASES if "tp8_share" not in c[0]} == {0, 1, 3, 4}
     shares = [c for c in bench.CONFIG_CASES if "tp8_share" in c[0]]
     assert shares and all(c[1] == 2 and (c[3], c[4], c[5]) == (24 // 8, 8 // 8, 128) for c in shares)
+
+
+def test_traffic_profile_matches_the_planned_decode_launch():
+    # roofline.traffic comes from profiles/decode_b1_hbm_traffic.md: its counts
+    # must belong to the launch the library plans now (host arithmetic only)
+    plan = bench.decode_plan()
+    got = bench.measured_traffic(plan)
+    assert got["profile_plan"] == plan, (got["profile_plan"], plan)
+    assert got["stale"] is False and got["bytes"] is not None
+    # within a few percent of the algorithmic bytes of one launch
+    assert 1.0 <= got["bytes"] / bench.decode_bytes(8193) < 1.1
+
+
+def test_stale_traffic_profile_is_withheld():
+    plan = dict(bench.decode_plan())
+    plan["splits"] += 1
+    got = bench.measured_traffic(plan)
+    assert got["stale"] is True and got["bytes"] is None
