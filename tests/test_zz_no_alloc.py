@@ -103,3 +103,54 @@ def test_noalloc_decode_step_rejects_partials_beyond_the_array(gpu):
     with pytest.raises(gpu.ShapeError):
         s.decode_step_noalloc(None, q, q, q, caches, gpu.KvAttentionConfig(1, Hq, Hq, D, True), out)
     assert all(c.len() == 0 for c in caches)
+
+
+def test_noalloc_decode_step_under_graph_capture(gpu):
+    """The use the entry point is for: one call captured into a HIP graph on a
+    fresh session (no call before the capture), then replayed three times
+    with eager work and synchronisation between the replays. Every replay
+    matches the workspace step on an identical cache (1e-4) and the previous
+    replay (bitwise); the appended row is the workspace step's, bitwise."""
+    import torch
+
+    from spissa_amd.device import Session
+
+    print("[case] noalloc decode step captured in a graph, 3 replays", flush=True)
+    Hq, Hkv, D, P = 24, 8, 128, 8192
+    stream = torch.cuda.Stream()
+    s = Session(0, stream=stream)
+    table = s.rope_table(_ffi.ROPE_LLAMA, D, 500000.0, max_positions=P + 8)
+    ca, cb = make_caches(s, Hkv, D, [P], P + 1, 36)
+    q = torch.from_numpy(normal_f32(seed_for(36, 99, 0, "q"), Hq * D)).cuda()
+    k = torch.from_numpy(normal_f32(seed_for(36, 99, 0, "k"), Hkv * D)).cuda()
+    v = torch.from_numpy(normal_f32(seed_for(36, 99, 0, "v"), Hkv * D)).cuda()
+    out_g = torch.full((Hq * D,), float("nan"), device="cuda")
+    out_w = torch.full((Hq * D,), float("nan"), device="cuda")
+    cfg = gpu.KvAttentionConfig(1, Hq, Hkv, D, True, 0)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        s.decode_step_noalloc(table, q, k, v, cb, cfg, out_g)
+    assert cb[0].len() == P + 1  # the host length advanced at capture
+    s.decode_step(table, q, k, v, ca, cfg, out_w)
+    s.sync()
+    want = out_w.cpu().numpy()
+    prev = None
+    for r in range(3):
+        out_g.fill_(float("nan"))  # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        s.sync()
+        got = out_g.cpu().numpy()
+        assert np.all(np.isfinite(got)), r
+        err = rel_err(got, want)
+        print(f"[noalloc graph] replay {r}: rel err vs workspace step {err:.2e}", flush=True)
+        assert err <= DECODE_TOL, r
+        if prev is not None:
+            assert np.array_equal(got.view(np.uint32), prev.view(np.uint32)), r
+        prev = got
+    w = Hkv * D
+    assert_bitwise(cb[0].keys()[P * w:], ca[0].keys()[P * w:], "appended key")
+    assert_bitwise(cb[0].values()[P * w:], ca[0].values()[P * w:], "appended value")
+    del g
