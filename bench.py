@@ -1246,8 +1246,9 @@ def main() -> int:
                               "from the current launch",
             "traffic_plan": traffic["profile_plan"],
             "plan": plan,
-            "kernel": "one decode attention launch = decode_split_kernel<128,3,3> + decode_combine_kernel<128,3>; "
-                      "event-timed average over 28 back-to-back launches per graph replay",
+            "kernel": "one decode attention launch = decode_split_kernel<128,3,3> + "
+                      "decode_combine_kernel<128,3,16,256>; event-timed average over 28 back-to-back launches "
+                      "per graph replay",
         },
         "device": res.get("device"),
     }
