@@ -998,6 +998,8 @@ def configs_only(args) -> dict:
             out["projections"] = projection_bench(sess, stream, gen, dev, args, time_graph)
         if "prefill_4096" in names:
             out.update(prefill_bench(sess, stream, gen, dev, args, time_graph))
+        if "workloads" in names:
+            out["workloads"] = workloads_bench(sess, stream, gen, dev, args, time_graph)
     return out
 
 
@@ -1199,8 +1201,8 @@ def main() -> int:
                     help="also run a 256 MiB device copy (HBM-counter calibration under rocprofv3 --pmc)")
     ap.add_argument("--configs", default="",
                     help="only time these comma-separated cases of CONFIG_CASES (and 'projections': the "
-                         "q/k/v projection at batch 1, 16 and 4096; 'prefill_4096': config 2a's prefill) and "
-                         "print their records (for counter passes); the benchmark line is not printed")
+                         "q/k/v projection at batch 1, 16 and 4096; 'prefill_4096': config 2a's prefill; 'workloads': "
+                         "the whole Gemma workloads) and print their records; the benchmark line is not printed")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build's attention path has no multi-GPU leg "

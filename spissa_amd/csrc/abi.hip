@@ -984,10 +984,12 @@ static bool plan_decode(int D, int Hq, int Hkv, size_t window, const int *past, 
   const size_t entry = (size_t)p->RB * (D + 2) * sizeof(float);
   // The new token gets a split of its own, dispatched first, so that its
   // loads, QK-norm and append run beside the streaming splits -- when the
-  // whole grid fits one round of workgroup slots (measured: the Gemma decode
-  // layers 9-11% faster; at batch 16 the extra workgroups unbalance the
-  // streaming ones, 183 against 168 us) and a fixed partial buffer holds two
-  // entries per group. Otherwise split 0 takes it after its cached rows.
+  // whole grid stays within kDecodeGridWorkgroups (measured: the Gemma decode
+  // layers 9-11% faster; past it the token workgroups cost more than they
+  // save: batch 16, 640 against 512 workgroups, 205 against 171 us; Llama-3.2-1B
+  // at 2048 keys, 520 against 512, 8.4 against 8.1 us) and a fixed partial
+  // buffer holds two entries per group. Otherwise split 0 takes it after its
+  // cached rows.
   int split_cap = kMaxDecodeSplits;
   p->tok_split = 1;
   if (partial_cap) {
@@ -998,7 +1000,7 @@ static bool plan_decode(int D, int Hq, int Hkv, size_t window, const int *past, 
   }
   p->kps = decode_keys_per_split(D, p->RB, total_rows, std::max(1, max_keys), split_cap - p->tok_split);
   const int cached_splits = (max_keys + p->kps - 1) / p->kps;
-  if (groups * (size_t)(cached_splits + 1) > (size_t)kDecodeRoundWorkgroups) p->tok_split = 0;
+  if (groups * (size_t)(cached_splits + 1) > (size_t)kDecodeGridWorkgroups) p->tok_split = 0;
   p->max_splits = p->tok_split ? cached_splits + 1 : std::max(1, cached_splits);
   p->workgroups = groups * p->max_splits;
   p->partial_bytes = groups * p->max_splits * entry;

@@ -20,9 +20,13 @@ enum : int { kDevErrSoftmaxDenominator = 1 };
 constexpr int kMaxDecodeBatch = 16;
 // Most key splits of one (sequence, KV head) the decode combine reads.
 constexpr int kMaxDecodeSplits = 512;
-// Workgroups of one round of the decode split kernel (4 per CU on 256 CUs),
-// the size decode_keys_per_split aims the grid at.
-constexpr int kDecodeRoundWorkgroups = 1024;
+// Most workgroups a decode launch aims at, token splits included: two per CU
+// on 256 CUs. Split-kernel grids a few workgroups past it ran far slower than
+// grids just under it (Gemma-3-4B's global layer at 16512 keys: 520 against
+// 464 workgroups, 34.5 against 27.4 us per layer), and grids of 3-4 per CU
+// (Llama-3.2-3B at 8192 keys, 696 workgroups: 17.3 us) slower than 2 (464:
+// 16.3 us).
+constexpr int kDecodeGridWorkgroups = 512;
 // Prefill key tiles are at most this wide; the staging buffer starts at a
 // multiple of it.
 constexpr int kPrefillTileAlign = 64;

@@ -157,7 +157,7 @@ def test_llama3b_decode_step_at_8192_batch1(gpu):
     Hq, Hkv, D, P, theta = 24, 8, 128, 8192, 500000.0
     cfg = KvAttentionConfig(1, Hq, Hkv, D, True)
     plan = plan_attention(cfg, [P])
-    assert plan["token_split"] == 1 and plan["splits"] > 64  # the form the bench times
+    assert plan["token_split"] == 1 and plan["splits"] > 32 and plan["workgroups"] <= 512  # the form the bench times
     s = Session(0)
     table = s.rope_table(_ffi.ROPE_LLAMA, D, theta, max_positions=P + 64)
     for layer in range(3):
