@@ -167,12 +167,12 @@ struct Geom {
 };
 
 // S^T of one key tile for the wave's QB query blocks over the 16-dim steps
-// [T0, T1): the first step starts from the row bias (BIAS: every element of
-// bias[qb] is minus the row's exponent reference) or from s (a masked tile's
-// start, already in s); later ones accumulate; kbuf is the K tile in LDS.
-template <int D, int BN, int QB, int T0, int T1, bool BIAS, int NT>
+// [T0, T1), accumulated onto s (which the first step finds holding minus the
+// row's exponent reference, or -inf for a masked tile's hidden keys); kbuf is
+// the K tile in LDS.
+template <int D, int BN, int QB, int T0, int T1, int NT>
 __device__ __forceinline__ void score_tile(f32x16 (&s)[QB][BN / 32], const char *kbuf, const unsigned (&k_rd)[NT],
-                                           const bf16x8 (&qf)[QB][NT], const f32x16 (&bias)[QB]) {
+                                           const bf16x8 (&qf)[QB][NT]) {
   constexpr int KB = BN / 32;
 #pragma unroll
   for (int tt = T0; tt < T1; ++tt)
@@ -180,10 +180,8 @@ __device__ __forceinline__ void score_tile(f32x16 (&s)[QB][BN / 32], const char 
     for (int kb = 0; kb < KB; ++kb) {
       const bf16x8 kf = *reinterpret_cast<const bf16x8 *>(kbuf + kb * 64 * D + k_rd[tt]);
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) {
-        const f32x16 acc = (BIAS && tt == T0) ? bias[qb] : s[qb][kb];
-        s[qb][kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[qb][tt], acc, 0, 0, 0);
-      }
+      for (int qb = 0; qb < QB; ++qb)
+        s[qb][kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[qb][tt], s[qb][kb], 0, 0, 0);
     }
 }
 
@@ -394,17 +392,18 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
   // Exponent reference per row: exponentials of a tile are taken against ms
   // (m, or 0 while m = -inf); m rises by more than kRescaleSlack (eager) or
   // when a tile's probabilities sum past kRaiseSum (lazy). The
-  // score MFMAs start from bias = -ms, so a score accumulator holds
+  // score MFMAs start from -ms, so a score accumulator holds
   // (scaled score - ms) and its exponential needs no subtraction.
   float ms[QB];
-  f32x16 bias[QB];
-  // Masking: the score accumulators of a masked tile start at -inf for the
-  // keys a row does not see (-ms elsewhere), so the MFMAs produce -inf there
-  // and the maxima and exponentials need no selects; unmasked tiles start
-  // from the bias registers. Score element i of block kb is key
-  // kb*32 + 8(i/4) + 4hl + i%4 of its tile. (Keys beyond the last one are zero
-  // padding, so -inf + finite stays -inf.) This issues the first 16-dim step
-  // of S(t); score_tile<..., 1, DT, false> adds the rest.
+  // The score accumulators start at -ms, written into them before the first
+  // MFMA (a block of -ms kept in 16 VGPRs across steps left no room for the
+  // LDS reads that the step's schedule runs ahead, at 243 of 256). A masked
+  // tile's accumulators start at -inf for the keys a row does not see, so the
+  // MFMAs produce -inf there and the maxima and exponentials need no selects.
+  // Score element i of block kb is key kb*32 + 8(i/4) + 4hl + i%4 of its tile.
+  // (Keys beyond the last one are zero padding, so -inf + finite stays -inf.)
+  // This issues the first 16-dim step of S(t); score_tile<..., 1, DT> adds the
+  // rest.
   auto score_first = [&](f32x16 (&s)[QB][KB], const char *kbuf, int t) {
     if (tile_masked(t)) {
       const int kt0 = t * BN;
@@ -419,10 +418,15 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
             s[qb][kb][i] = (kk < lo || kk > hi) ? NEG_INF : -ms[qb];
           }
       }
-      score_tile<D, BN, QB, 0, 1, false>(s, kbuf, k_rd, qf, bias);
     } else {
-      score_tile<D, BN, QB, 0, 1, true>(s, kbuf, k_rd, qf, bias);
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) s[qb][kb][i] = -ms[qb];
     }
+    score_tile<D, BN, QB, 0, 1>(s, kbuf, k_rd, qf);
   };
   // Row maxima of a score tile (log2 domain, the reference added back).
   auto row_max = [&](const f32x16 (&s)[QB][KB], float (&mx)[QB]) {
@@ -474,14 +478,32 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
         pf[qb][ks] = p;
       }
     }
-    score_tile<D, BN, QB, 1, DT, false>(nxt, k_next, k_rd, qf, bias);
+    score_tile<D, BN, QB, 1, DT>(nxt, k_next, k_rd, qf);
+    if constexpr (QB == 1) {
+      // Schedule of part A: three K fragments read ahead of the score MFMAs,
+      // then per MFMA one more read and up to eight VALU operations of the
+      // exponentials. Left to itself the compiler reads one fragment ahead
+      // here and two in part B, and the MFMAs wait on LDS: with both
+      // schedules the 4096-token causal layer (the reference-order call)
+      // went from 121.7 to 118.4 us on one box.
+      constexpr int NM = KB * (DT - 1);
+      __builtin_amdgcn_sched_group_barrier(0x100, 3, 1);  // DS reads
+#pragma unroll
+      for (int i = 0; i < NM - 3; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);  // DS read
+        __builtin_amdgcn_sched_group_barrier(0x002, 8, 1);  // VALU
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 3, 1);
+    }
 
     if constexpr (LAZY) {
     // The exponent reference is raised lazily: only a row whose probabilities
     // grew large (a lane's sum above 2^16, i.e. scores well above the
     // reference) or that has seen no key yet takes the exact maximum of tile
     // t, rescales O and its sum, recomputes the tile's probabilities and
-    // shifts the bias of S(t+1). No per-tile row maximum is needed otherwise.
+    // shifts S(t+1), which started from the old reference. No per-tile row
+    // maximum is needed otherwise.
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
       const bool hot = (psum[qb] > kRaiseSum) | (m[qb] == NEG_INF);
@@ -517,8 +539,6 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
         for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
           for (int i = 0; i < 16; ++i) nxt[qb][kb][i] -= shift;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) bias[qb][i] = -msn;
         m[qb] = mnew;
         ms[qb] = msn;
       }
@@ -540,6 +560,18 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
         for (int qb = 0; qb < QB; ++qb)
           oacc[qb][d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[qb][ks], oacc[qb][d], 0, 0, 0);
       }
+    if constexpr (QB == 1) {
+      // Schedule of part B: four V^T fragments read ahead of the PV MFMAs,
+      // then one read per MFMA (the default reads two ahead, and with no VALU
+      // work in this part every pair of MFMAs waits on LDS).
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS reads
+#pragma unroll
+      for (int i = 0; i < KS * DB - 4; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    }
     if constexpr (!LAZY) {
     const bool has_next = t + 1 < t_end;
     float mx[QB], alpha[QB], shift[QB];
@@ -571,8 +603,6 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
         for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
           for (int i = 0; i < 16; ++i) nxt[qb][kb][i] -= shift[qb];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) bias[qb][i] = -ms[qb];
       }
     }
     wait_copies();
@@ -588,13 +618,9 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
   wait_copies();
   copies_barrier();
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    ms[qb] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) bias[qb][i] = 0.0f;
-  }
+  for (int qb = 0; qb < QB; ++qb) ms[qb] = 0.0f;
   score_first(sa, k_lds0, t_begin);
-  score_tile<D, BN, QB, 1, DT, false>(sa, k_lds0, k_rd, qf, bias);
+  score_tile<D, BN, QB, 1, DT>(sa, k_lds0, k_rd, qf);
   {
     float mx[QB];
     row_max(sa, mx);
@@ -606,8 +632,6 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) sa[qb][kb][i] -= ms[qb];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) bias[qb][i] = -ms[qb];
     }
   }
   copies_barrier();  // every wave is done with K(t0) before K(t0+2) lands in its buffer
