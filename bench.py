@@ -904,8 +904,11 @@ def prefill_bench(sess, stream, gen, dev, args, time_graph) -> dict:
     f32 q/k/v passed in, no cache; the bf16 K/V operands are made inside the
     call, rotary.rs:335-415); prefill_step_4096 = the fused prefill step (RoPE,
     append of the f32 rows and bf16 operands, staged q, then attention);
-    prefill_attention_4096 = the step's attention launch alone over a cache
-    that already holds the prompt (the dominant kernel's MFMA rate)."""
+    prefill_attention_4096 = the attention call over a cache that already
+    holds the prompt (spissa_attention_cached_device: one launch, f32 q
+    rounded to bf16 in the kernel, K/V from each layer's bf16 shadow; the
+    dominant kernel's MFMA rate). Inside the fused step the same kernel reads
+    q already staged in bf16 and K/V the append just wrote, and runs faster."""
     import torch
 
     from spissa_amd import _ffi
@@ -935,7 +938,7 @@ def prefill_bench(sess, stream, gen, dev, args, time_graph) -> dict:
             sess.prefill_step(ptable, pq[l], pk[l], pv[l], pcaches[l], cfgp, po[l])
 
     def attention_phase():
-        # the step's attention launch alone: the prompt is already in the cache
+        # the attention call alone: the prompt is already in the cache
         for l in range(LAYERS):
             sess.attention_cached(pq[l], pcaches[l], cfgp, po[l])
 
@@ -1295,7 +1298,8 @@ def main() -> int:
                         "bf16 K/V operands are made inside the call)",
         "prefill_step_4096": "fused prefill step: RoPE + append of f32 rows and bf16 operands + staged q, then "
                              "attention",
-        "prefill_attention_4096": "the fused step's attention launch alone (the prompt already in the cache)",
+        "prefill_attention_4096": "the attention call over a cache already holding the prompt (one launch; f32 q, "
+                                  "K/V from the cache's bf16 shadow)",
     }
     for key, phase in phases.items():
         if key in res:
