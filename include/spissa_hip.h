@@ -271,7 +271,7 @@ typedef struct {
     int tiles_per_split;    /* prefill with key splits: key tiles per split */
     int tile_keys;          /* prefill: keys per tile */
     int workgroup_queries;  /* prefill: queries per workgroup */
-    int o_split;            /* always 0 (no kernel splits O over waves; kept for the struct's layout) */
+    int block_waves;        /* prefill: waves sharing one query block's key tiles (2 = wave pairs on alternate tiles) */
     int xcd_group;          /* prefill: 1 = with key splits, the workgroups of one KV head's split share an XCD;
                                2 = unsplit windowed, each XCD takes a contiguous run of query blocks */
     long max_tiles;         /* prefill: most key tiles one unsplit workgroup visits */

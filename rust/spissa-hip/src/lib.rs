@@ -101,7 +101,7 @@ pub mod sys {
         pub tiles_per_split: c_int,
         pub tile_keys: c_int,
         pub workgroup_queries: c_int,
-        pub o_split: c_int,
+        pub block_waves: c_int,
         pub xcd_group: c_int,
         pub max_tiles: c_long,
         pub workgroups: usize,

@@ -88,7 +88,7 @@ class AttentionPlanC(C.Structure):
     _fields_ = [
         ("path", C.c_int), ("heads_per_block", C.c_int), ("head_blocks", C.c_int),
         ("keys_per_split", C.c_int), ("splits", C.c_int), ("token_split", C.c_int), ("tiles_per_split", C.c_int),
-        ("tile_keys", C.c_int), ("workgroup_queries", C.c_int), ("o_split", C.c_int),
+        ("tile_keys", C.c_int), ("workgroup_queries", C.c_int), ("block_waves", C.c_int),
         ("xcd_group", C.c_int), ("max_tiles", C.c_long), ("workgroups", c_size), ("partial_bytes", c_size), ("stage_bytes", c_size),
     ]
 

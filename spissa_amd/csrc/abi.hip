@@ -1127,6 +1127,9 @@ static void plan_prefill(PrefillArgs &a, int D, int cus, PrefillPlan *p) {
   a.cap_stage = (long)p->cap_stage;
   a.splits = 1;
   a.tps = 0;
+  const long slots = (long)cus * prefill_wgs_per_cu(a, D);
+  a.ksp = 1;
+  a.ksp = prefill_wave_pairs(a, D, slots);
   // Key splits when the unsplit grid cannot fill the GPU (short chunks over
   // long caches, few heads): enough splits for one round of workgroup slots,
   // each covering at least four key tiles of its workgroup's range (eight
@@ -1134,10 +1137,16 @@ static void plan_prefill(PrefillArgs &a, int D, int cus, PrefillPlan *p) {
   // 16384 keys measured 23.4 us with 4 splits against 25.1 us with 9). The
   // splits cover the widest tile range any workgroup has, so every
   // workgroup's keys are covered.
+  // Causal head_dim-64/128 prompts (fewer cached keys than queries) run
+  // unsplit: their partials are as large as the output, and writing and
+  // merging them cost more than the idle slots (reference-order call per
+  // layer: Llama-3.2-1B 1024-token prompt 33.2 us with 2 splits against 24.2
+  // unsplit, 512 tokens 19.2 against 15.5; Llama-3.2-3B 1024 tokens 40.1
+  // with 3 splits against 33.7 unsplit).
+  const bool causal_prompt = a.causal && a.P < a.S;
   const long base = prefill_base_workgroups(a, D);
-  const long slots = (long)cus * prefill_wgs_per_cu(a, D);
   p->tiles = prefill_max_tile_span(a, D);
-  if (base < slots) {
+  if (base < slots && !(D < 256 && causal_prompt)) {
     const long min_tiles = D >= 256 && a.window > 0 ? 8 : 4;
     const long want = std::min(std::min((slots + base - 1) / base, p->tiles / min_tiles), (long)D);
     if (want >= 2) {  // (at most head_dim splits: the measured useful range)
@@ -1542,7 +1551,7 @@ extern "C" int spissa_plan_attention(const spissa_kv_attention_config *cfg, cons
     out->workgroup_queries = prefill_wg_queries(a, D);
     out->heads_per_block = prefill_wg_heads(a, D);
     out->head_blocks = a.R / out->heads_per_block;
-    out->o_split = 0;
+    out->block_waves = a.ksp == 2 ? 2 : 1;
     out->xcd_group = a.xcd_group;
     out->max_tiles = p.tiles;
     out->workgroups = p.workgroups;

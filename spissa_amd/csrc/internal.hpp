@@ -131,6 +131,11 @@ struct PrefillArgs {
   // the workgroup order (the grid is padded to a multiple of 8).
   // prefill_use_xcd_group decides.
   int xcd_group;
+  // Waves per query block that share its key tiles (1 or 2): with 2, the two
+  // waves of a pair take alternate 64-key tiles of the same queries and merge
+  // their (m, l, O) through LDS at the end, halving the longest causal
+  // blocks' serial tile chain. prefill_wave_pairs decides.
+  int ksp;
 };
 
 // Workgroup slots per CU and key-tile width of the prefill kernels, and the
@@ -147,6 +152,7 @@ long prefill_max_tile_span(const PrefillArgs &a, int D);
 // (grouped by XCD: units of one KV head and split padded to a multiple of 8).
 long prefill_grid_workgroups(long n_qblocks, long head_blocks, long Hkv, long splits, int xcd_group);
 int prefill_use_xcd_group(const PrefillArgs &a, int D);
+int prefill_wave_pairs(const PrefillArgs &a, int D, long slots);
 
 struct GenericArgs {
   const float *q;  // [S, Hq, D]

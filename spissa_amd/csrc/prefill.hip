@@ -199,11 +199,14 @@ __device__ __forceinline__ float sum_bf16x8(const bf16x8 p) {
 
 // Head_dim 64 and 128. QB query blocks of 32 per wave (1 in the launched
 // shapes); two waves per SIMD (the second __launch_bounds__ argument is the
-// minimum waves per SIMD: at most 256 VGPRs each).
-template <int D, int RB, int NPB, int BN, int QB>
-__global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillArgs a) {
+// minimum waves per SIMD: at most 256 VGPRs each). KSP waves share each
+// query block's key tiles (wave pairs: tile 2T + kh of super-tile T goes to
+// wave kh of the pair).
+template <int D, int RB, int NPB, int BN, int QB, int KSP>
+__global__ __launch_bounds__(RB *NPB *KSP * 64, 2) void prefill_kernel(const PrefillArgs a) {
   static_assert(D <= 128, "head_dim 256 runs prefill_q16_kernel");
-  constexpr int NW = RB * NPB;
+  static_assert(KSP == 1 || KSP == 2, "one wave or a wave pair per query block");
+  constexpr int NW = RB * NPB * KSP;
   constexpr int WQ = QB * 32;  // queries per wave
   constexpr int WGQ = NPB * WQ;
   using G = Geom<D, BN, NW>;
@@ -216,10 +219,11 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
   // Four separate LDS objects (not one array): the compiler then knows that
   // copies into one buffer do not alias reads of another and does not wait
   // for the copies before every LDS read.
-  __shared__ __attribute__((aligned(1024))) char k_lds0[G::KBYTES];
-  __shared__ __attribute__((aligned(1024))) char k_lds1[G::KBYTES];
-  __shared__ __attribute__((aligned(1024))) char v_lds0[G::VBYTES];
-  __shared__ __attribute__((aligned(1024))) char v_lds1[G::VBYTES];
+  // (With wave pairs each buffer holds the KSP tiles of a super-tile.)
+  __shared__ __attribute__((aligned(1024))) char k_lds0[KSP * G::KBYTES];
+  __shared__ __attribute__((aligned(1024))) char k_lds1[KSP * G::KBYTES];
+  __shared__ __attribute__((aligned(1024))) char v_lds0[KSP * G::VBYTES];
+  __shared__ __attribute__((aligned(1024))) char v_lds1[KSP * G::VBYTES];
 
   const int HB = a.R / RB;
   int h, hb, split, qt;
@@ -253,7 +257,8 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
   // The wave index is uniform: readfirstlane keeps it (and all that derives
   // from it) in scalar registers and wave-level branches uniform.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int r = wave % RB, pb = wave / RB;
+  const int kh = wave % KSP, wq = wave / KSP;  // tile parity within the pair; the pair
+  const int r = wq % RB, pb = wq / RB;
   const int head = h * a.R + hb * RB + r;
   const int p0 = qt * WGQ;
   const int wp0 = p0 + pb * WQ;
@@ -272,13 +277,17 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
   }
   if (t_begin >= t_end) {  // this split sees none of the workgroup's keys (uniform exit)
     const int pos = wp0 + lane;
-    if (lane < WQ && pos < a.S) {
+    if (kh == 0 && lane < WQ && pos < a.S) {
       float *ml = a.part_ml + (((long)split * a.S + pos) * a.Hq + head) * 2;
       ml[0] = -__builtin_inff();
       ml[1] = 0.0f;
     }
     return;
   }
+  // Super-tiles of KSP tiles: T covers tiles [KSP*T, KSP*T + KSP). Wave kh of
+  // a pair scores tile KSP*T + kh; a tile outside [t_begin, t_end) is hidden
+  // from it.
+  const int T_begin = t_begin / KSP, T_end = (t_end + KSP - 1) / KSP;
 
   // Q^T (B operand): lane holds query lq of block qb, dims 16t + 8hl + [0,8).
   // Q carries the softmax scale times log2(e), so the scores come out of the
@@ -356,19 +365,29 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
 
   // Tiles below P8 come from the cache shadow, the others from staging (P8 is
   // a multiple of the tile width, so the choice is uniform per tile).
-  auto copy_k = [&](int t, char *dst) {
-    const int nk = t * BN;
-    const char *src = nk < a.P8 ? kb_c + (long)nk * D * 2 : kb_s + (long)(nk - a.P8) * D * 2;
+  // (A super-tile's tiles past the range's last are copied as that last one:
+  // in bounds, and hidden from the wave that takes them.)
+  auto copy_k = [&](int T, char *dst) {
 #pragma unroll
-    for (int j = 0; j < G::KDMA; ++j) dma16_untracked(src, k_src(j), dst + (wave + j * NW) * 1024);
+    for (int i = 0; i < KSP; ++i) {
+      const int nk = (KSP == 1 ? T : min(KSP * T + i, t_end - 1)) * BN;
+      const char *src = nk < a.P8 ? kb_c + (long)nk * D * 2 : kb_s + (long)(nk - a.P8) * D * 2;
+#pragma unroll
+      for (int j = 0; j < G::KDMA; ++j)
+        dma16_untracked(src, k_src(j), dst + i * G::KBYTES + (wave + j * NW) * 1024);
+    }
   };
-  auto copy_v = [&](int t, char *dst) {
-    const int nk = t * BN;
-    const bool cached = nk < a.P8;
-    const char *src = cached ? vt_c + (long)nk * 2 : vt_s + (long)(nk - a.P8) * 2;
-    const unsigned stride = cached ? vt_stride_c : vt_stride_s;
+  auto copy_v = [&](int T, char *dst) {
 #pragma unroll
-    for (int j = 0; j < G::VDMA; ++j) dma16_untracked(src, v_src(j, stride), dst + (wave + j * NW) * 1024);
+    for (int i = 0; i < KSP; ++i) {
+      const int nk = (KSP == 1 ? T : min(KSP * T + i, t_end - 1)) * BN;
+      const bool cached = nk < a.P8;
+      const char *src = cached ? vt_c + (long)nk * 2 : vt_s + (long)(nk - a.P8) * 2;
+      const unsigned stride = cached ? vt_stride_c : vt_stride_s;
+#pragma unroll
+      for (int j = 0; j < G::VDMA; ++j)
+        dma16_untracked(src, v_src(j, stride), dst + i * G::VBYTES + (wave + j * NW) * 1024);
+    }
   };
 
   // Visible keys [vis_lo, vis_hi] of this lane's two queries.
@@ -402,10 +421,19 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
   // MFMAs produce -inf there and the maxima and exponentials need no selects.
   // Score element i of block kb is key kb*32 + 8(i/4) + 4hl + i%4 of its tile.
   // (Keys beyond the last one are zero padding, so -inf + finite stays -inf.)
-  // This issues the first 16-dim step of S(t); score_tile<..., 1, DT> adds the
+  // This issues the first 16-dim step of S(t), t = KSP*T + kh, from the
+  // wave's tile of the super-tile in kbuf; score_tile<..., 1, DT> adds the
   // rest.
-  auto score_first = [&](f32x16 (&s)[QB][KB], const char *kbuf, int t) {
-    if (tile_masked(t)) {
+  auto score_first = [&](f32x16 (&s)[QB][KB], const char *kbuf, int T) {
+    const int t = KSP * T + kh;
+    if (KSP > 1 && (t < t_begin || t >= t_end)) {
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) s[qb][kb][i] = NEG_INF;
+    } else if (tile_masked(t)) {
       const int kt0 = t * BN;
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
@@ -426,7 +454,7 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
 #pragma unroll
           for (int i = 0; i < 16; ++i) s[qb][kb][i] = -ms[qb];
     }
-    score_tile<D, BN, QB, 0, 1>(s, kbuf, k_rd, qf);
+    score_tile<D, BN, QB, 0, 1>(s, kbuf + kh * G::KBYTES, k_rd, qf);
   };
   // Row maxima of a score tile (log2 domain, the reference added back).
   auto row_max = [&](const f32x16 (&s)[QB][KB], float (&mx)[QB]) {
@@ -441,8 +469,8 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
     }
   };
 
-  // One pipelined step on tile t (scores in `cur`, exponent reference ms
-  // already covering tile t, O and l already scaled to it):
+  // One pipelined step on (super-)tile t (scores in `cur`, exponent
+  // reference ms already covering tile t, O and l already scaled to it):
   //   copies of K(t+2) and V(t+1) go out;
   //   part A: the probabilities of tile t on the VALU next to the MFMAs of
   //     S(t+1) = K(t+1) Q^T (unconditional: on the last tile it reads a
@@ -450,15 +478,17 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
   //   part B: O^T += V(t)^T P(t)^T on the MFMAs next to the row maxima of
   //     tile t+1, which set the exponent reference of the next step;
   //   the (rare) rescale of O, after the PV MFMAs; one barrier.
-  // O selects the buffers.
+  // O selects the buffers; a wave reads its own tile of each super-tile.
   auto step = [&](auto O_, int t, f32x16 (&cur)[QB][KB], f32x16 (&nxt)[QB][KB]) {
     constexpr int O = decltype(O_)::value;
     char *const k_this = O ? k_lds1 : k_lds0;  // receives K(t+2)
     char *const k_next = O ? k_lds0 : k_lds1;  // holds K(t+1)
     char *const v_this = O ? v_lds1 : v_lds0;  // holds V(t)
     char *const v_next = O ? v_lds0 : v_lds1;  // receives V(t+1)
-    if (t + 2 < t_end) copy_k(t + 2, k_this);
-    if (t + 1 < t_end) copy_v(t + 1, v_next);
+    const char *const k_mine = k_next + kh * G::KBYTES;
+    const char *const v_mine = v_this + kh * G::VBYTES;
+    if (t + 2 < T_end) copy_k(t + 2, k_this);
+    if (t + 1 < T_end) copy_v(t + 1, v_next);
     score_first(nxt, k_next, t + 1);
 
     // Part A.
@@ -478,7 +508,7 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
         pf[qb][ks] = p;
       }
     }
-    score_tile<D, BN, QB, 1, DT>(nxt, k_next, k_rd, qf);
+    score_tile<D, BN, QB, 1, DT>(nxt, k_mine, k_rd, qf);
     if constexpr (QB == 1) {
       // Schedule of part A: three K fragments read ahead of the score MFMAs,
       // then per MFMA one more read and up to eight VALU operations of the
@@ -555,7 +585,7 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
       for (int d = 0; d < DB; ++d) {
-        const bf16x8 vf = *reinterpret_cast<const bf16x8 *>(v_this + d * 64 * BN + v_rd[ks]);
+        const bf16x8 vf = *reinterpret_cast<const bf16x8 *>(v_mine + d * 64 * BN + v_rd[ks]);
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb)
           oacc[qb][d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[qb][ks], oacc[qb][d], 0, 0, 0);
@@ -573,7 +603,7 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
       __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
     }
     if constexpr (!LAZY) {
-    const bool has_next = t + 1 < t_end;
+    const bool has_next = t + 1 < T_end;
     float mx[QB], alpha[QB], shift[QB];
     bool raise[QB];
     row_max(nxt, mx);
@@ -611,16 +641,16 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
 
   // Prologue: K(t0), V(t0), K(t0+1) copied; S(t0) and its row maxima.
   f32x16 sa[QB][KB], sb[QB][KB];
-  copy_k(t_begin, k_lds0);
-  copy_v(t_begin, v_lds0);
-  if (t_begin + 1 < t_end) copy_k(t_begin + 1, k_lds1);
+  copy_k(T_begin, k_lds0);
+  copy_v(T_begin, v_lds0);
+  if (T_begin + 1 < T_end) copy_k(T_begin + 1, k_lds1);
   load_q();
   wait_copies();
   copies_barrier();
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) ms[qb] = 0.0f;
-  score_first(sa, k_lds0, t_begin);
-  score_tile<D, BN, QB, 1, DT>(sa, k_lds0, k_rd, qf);
+  score_first(sa, k_lds0, T_begin);
+  score_tile<D, BN, QB, 1, DT>(sa, k_lds0 + kh * G::KBYTES, k_rd, qf);
   {
     float mx[QB];
     row_max(sa, mx);
@@ -636,9 +666,46 @@ __global__ __launch_bounds__(RB *NPB * 64, 2) void prefill_kernel(const PrefillA
   }
   copies_barrier();  // every wave is done with K(t0) before K(t0+2) lands in its buffer
 
-  for (int t = t_begin; t < t_end; t += 2) {
+  for (int t = T_begin; t < T_end; t += 2) {
     step(std::integral_constant<int, 0>(), t, sa, sb);
-    if (t + 1 < t_end) step(std::integral_constant<int, 1>(), t + 1, sb, sa);
+    if (t + 1 < T_end) step(std::integral_constant<int, 1>(), t + 1, sb, sa);
+  }
+
+  if constexpr (KSP == 2) {
+    // The pair's odd wave hands (O, m, l) of its tiles to the even wave
+    // through LDS (the K buffers: the last step's barrier has passed every
+    // read of them, and no copy is in flight), which merges them onto its own
+    // against the larger maximum; m = -inf (no key seen) contributes nothing.
+    // Layout [value][lane], one float per lane per value.
+    constexpr int NX = QB * (DB * 16 + 2);
+    static_assert(NX * 64 * 4 <= KSP * G::KBYTES && RB * NPB <= 2, "pair exchange fits one K buffer per pair");
+    float *xch = reinterpret_cast<float *>(wq == 0 ? k_lds0 : k_lds1) + lane;
+    if (kh == 1) {
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+#pragma unroll
+        for (int d = 0; d < DB; ++d)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) xch[((qb * DB + d) * 16 + i) * 64] = oacc[qb][d][i];
+        xch[(QB * DB * 16 + 2 * qb) * 64] = m[qb];
+        xch[(QB * DB * 16 + 2 * qb + 1) * 64] = l[qb];
+      }
+    }
+    __syncthreads();
+    if (kh == 1) return;
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const float m1 = xch[(QB * DB * 16 + 2 * qb) * 64], l1 = xch[(QB * DB * 16 + 2 * qb + 1) * 64];
+      const float M = m[qb] > m1 ? m[qb] : m1;
+      const float f0 = m[qb] == NEG_INF ? 0.0f : fast_exp2(m[qb] - M);
+      const float f1 = m1 == NEG_INF ? 0.0f : fast_exp2(m1 - M);
+      l[qb] = l[qb] * f0 + l1 * f1;
+#pragma unroll
+      for (int d = 0; d < DB; ++d)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) oacc[qb][d][i] = oacc[qb][d][i] * f0 + xch[((qb * DB + d) * 16 + i) * 64] * f1;
+      m[qb] = M;
+    }
   }
 
   if (a.splits > 1) {  // unnormalised O and (m, l) of this key split
@@ -1169,13 +1236,13 @@ hipError_t launch_q16(hipStream_t st, PrefillArgs a) {
   return hipGetLastError();
 }
 
-template <int D, int RB, int NPB, int BN, int QB>
+template <int D, int RB, int NPB, int BN, int QB, int KSP>
 hipError_t launch_shape(hipStream_t st, PrefillArgs a) {
   constexpr int WGQ = NPB * QB * 32;
   a.n_qblocks = (a.S + WGQ - 1) / WGQ;
   const long blocks = prefill_grid_workgroups(a.n_qblocks, a.R / RB, a.Hkv, a.splits, a.xcd_group);
-  hipLaunchKernelGGL((prefill_kernel<D, RB, NPB, BN, QB>), dim3((unsigned)blocks), dim3(RB * NPB * 64), 0,
-                     st, a);
+  hipLaunchKernelGGL((prefill_kernel<D, RB, NPB, BN, QB, KSP>), dim3((unsigned)blocks), dim3(RB * NPB * KSP * 64),
+                     0, st, a);
   return hipGetLastError();
 }
 
@@ -1185,12 +1252,20 @@ hipError_t launch_shape(hipStream_t st, PrefillArgs a) {
 // MFMA but, at head_dim 128, needs more than 256 VGPRs and measured slower;
 // at head_dim 64 it halves the workgroup count, which a 2048-token prefill
 // cannot afford.)
+// Wave pairs (head_dim 64, prefill_wave_pairs): two heads, or one head with
+// two blocks, each block's key tiles split between the two waves of a pair.
 template <int D>
 hipError_t launch_r(hipStream_t st, const PrefillArgs &a) {
   constexpr int BN = 64;
-  if (a.R % 4 == 0) return launch_shape<D, 4, 1, BN, 1>(st, a);
-  if (a.R % 2 == 0) return launch_shape<D, 2, 2, BN, 1>(st, a);
-  return launch_shape<D, 1, 4, BN, 1>(st, a);
+  if constexpr (D == 64) {
+    if (a.ksp == 2) {
+      if (a.R % 2 == 0) return launch_shape<D, 2, 1, BN, 1, 2>(st, a);
+      return launch_shape<D, 1, 2, BN, 1, 2>(st, a);
+    }
+  }
+  if (a.R % 4 == 0) return launch_shape<D, 4, 1, BN, 1, 1>(st, a);
+  if (a.R % 2 == 0) return launch_shape<D, 2, 2, BN, 1, 1>(st, a);
+  return launch_shape<D, 1, 4, BN, 1, 1>(st, a);
 }
 
 // head_dim 256: four waves of 16 queries, 32-key tiles: four heads, two heads
@@ -1225,8 +1300,29 @@ bool prefill_supported(int D) { return D == 64 || D == 128 || D == 256; }
 // Workgroups of four waves (launch_r, launch_r16 above): four heads, two
 // heads with two query blocks, or one head with four blocks; a wave's block is
 // 32 queries (16 at head_dim 256), so a workgroup covers 128 query rows (64).
-int prefill_wg_heads(const PrefillArgs &a, int) { return a.R % 4 == 0 ? 4 : a.R % 2 == 0 ? 2 : 1; }
-int prefill_wg_queries(const PrefillArgs &a, int D) { return (D >= 256 ? 64 : 128) / prefill_wg_heads(a, D); }
+// With wave pairs (a.ksp == 2) two waves share a block: two heads, or one
+// head with two blocks.
+int prefill_wg_heads(const PrefillArgs &a, int) {
+  if (a.ksp == 2) return a.R % 2 == 0 ? 2 : 1;
+  return a.R % 4 == 0 ? 4 : a.R % 2 == 0 ? 2 : 1;
+}
+int prefill_wg_queries(const PrefillArgs &a, int D) {
+  return (D >= 256 ? 64 : 128) / (prefill_wg_heads(a, D) * (a.ksp == 2 ? 2 : 1));
+}
+// Wave pairs for causal head_dim-64 prompts (fewer cached keys than
+// queries) whose paired grid still fits one round of workgroup slots: there
+// the longest query blocks' tile chain sets the launch time, and a pair
+// halves it. A pair's workgroup covers half the heads, so each K/V tile copy
+// serves half the waves: with a second round of workgroups that costs more
+// than the chain saves. Llama-3.2-1B (32/8 heads) prompts, reference-order
+// call per layer: 1024 tokens 24.2 -> 21.2 us, 512 15.5 -> 13.9 us, 256
+// 12.0 -> 11.0 us; 2048 tokens (two rounds paired) 42.9 against 46.1 us.
+int prefill_wave_pairs(const PrefillArgs &a, int D, long slots) {
+  if (D != 64 || !a.causal || a.window > 0 || a.S < 2 * 64 || a.P >= a.S) return 1;
+  PrefillArgs b = a;
+  b.ksp = 1;
+  return 2 * prefill_base_workgroups(b, D) <= slots ? 2 : 1;
+}
 // Windowed head_dim-256 layers run the four-stage kernel (128 KB of LDS).
 int prefill_wgs_per_cu(const PrefillArgs &a, int D) { return D >= 256 && a.window > 0 ? 1 : 2; }
 int prefill_tile_keys(int D) { return D >= 256 ? 32 : 64; }  // BN of launch_d

@@ -82,6 +82,26 @@ def test_prefill_bf16_parity(gpu, name, S, P, Hq, Hkv, D, window):
     assert rel_err(got, ref) <= BF16_TOL
 
 
+@pytest.mark.parametrize("S,P,Hq,Hkv", [
+    (1024, 0, 32, 8),  # Llama-3.2-1B heads (R = 4: two heads per workgroup)
+    (333, 0, 16, 8),   # R = 2
+    (700, 0, 24, 8),   # R = 3: one head, two query blocks per workgroup
+    (129, 7, 8, 8),    # R = 1, a few cached keys, an odd tile count
+])
+def test_prefill_wave_pairs(gpu, S, P, Hq, Hkv):
+    """Head_dim-64 causal prompts run wave pairs (two waves take alternate
+    key tiles of one query block and merge through LDS); every head grouping
+    of the pair launcher against the oracle."""
+    from spissa_amd.device import plan_attention
+
+    D = 64
+    plan = plan_attention(gpu.KvAttentionConfig(S, Hq, Hkv, D, True, 0), [P])
+    print(f"[case] prefill wave pairs S={S} P={P} Hq={Hq} Hkv={Hkv} plan={plan['block_waves']}", flush=True)
+    assert plan["block_waves"] == 2
+    got, ref, _, _ = run_both(gpu, 31, S, S, P, Hq, Hkv, D)
+    assert rel_err(got, ref) <= BF16_TOL
+
+
 def test_prefill_non_causal(gpu):
     got, ref, _, _ = run_both(gpu, 13, 0, 64, 20, 8, 2, 128, 0, causal=False)
     assert rel_err(got, ref) <= BF16_TOL

@@ -143,9 +143,10 @@ def check_prefill(cfg, P, plan):
     assert TILE_ALIGN % BN == 0
     key_total = P + S
     n_qblocks = -(-S // WGQ)
-    rb = plan["heads_per_block"]
-    # four waves per workgroup of 32 queries each (16 at head_dim 256)
-    assert rb * WGQ == (64 if D >= 256 else 128)
+    rb, kw = plan["heads_per_block"], plan["block_waves"]
+    # four waves per workgroup of 32 queries each (16 at head_dim 256); wave
+    # pairs (kw = 2) put two waves on each block
+    assert kw in (1, 2) and rb * WGQ * kw == (64 if D >= 256 else 128)
     assert plan["head_blocks"] * rb == Hq // Hkv
     check_prefill_grid(plan, n_qblocks, Hkv, plan["head_blocks"], splits)
     P8 = P & ~(TILE_ALIGN - 1)
@@ -175,6 +176,19 @@ def check_prefill(cfg, P, plan):
             te = min(t_end, tb + tps) if splits > 1 else t_end
             seen.extend(range(tb, te))
         assert seen == list(range(t_begin, t_end)), (qt, t_begin, t_end, splits, tps)
+        # wave pairs: in each split, wave kh of the pair takes tile kw*T + kh of
+        # super-tiles T in [tb // kw, ceil(te / kw)), hidden outside [tb, te),
+        # and copies min(kw*T + i, te - 1): every tile once, every copy inside
+        for split in range(splits):
+            tb = t_begin + (split * tps if splits > 1 else 0)
+            te = min(t_end, tb + tps) if splits > 1 else t_end
+            if tb >= te:
+                continue
+            taken = sorted(kw * T + kh for T in range(tb // kw, -(-te // kw)) for kh in range(kw)
+                           if tb <= kw * T + kh < te)
+            assert taken == list(range(tb, te))
+            copied = {min(kw * T + i, te - 1) for T in range(tb // kw, -(-te // kw)) for i in range(kw)}
+            assert min(copied) >= tb - (kw - 1) and max(copied) == te - 1
         # staged rows the block reads stay inside the staging buffer
         if t_end * BN > P8:
             assert t_end * BN - P8 <= cap_stage
@@ -206,6 +220,12 @@ BASELINE_PREFILL = [  # (name, S, P, Hq, Hkv, D, window, causal)
     ("non-causal W512 over 4100", 256, 4100, 32, 8, 64, 512, False),
     ("non-causal W1024 over 8000", 512, 8000, 32, 8, 128, 1024, False),
     ("non-causal W256 d256", 200, 3000, 8, 4, 256, 256, False),
+    # wave pairs (head_dim-64 causal prompts): R = 4, 2, 3 and 1, ragged lengths
+    ("pairs llama-1B prompt 1024", 1024, 0, 32, 8, 64, 0, True),
+    ("pairs R=2 prompt 333", 333, 0, 16, 8, 64, 0, True),
+    ("pairs R=3 prompt 700", 700, 0, 24, 8, 64, 0, True),
+    ("pairs R=1 prompt 129 after 7", 129, 7, 8, 8, 64, 0, True),
+    ("llama-1B chunk 128 on 2048", 128, 2048, 32, 8, 64, 0, True),
 ]
 
 
@@ -306,3 +326,24 @@ def test_plan_paths():
     assert plan_attention(KvAttentionConfig(8, 6, 3, 128, True), [10],
                           precision=_ffi.PREFILL_F32)["path"] == _ffi.KERNEL_GENERIC
     assert plan_attention(KvAttentionConfig(8, 6, 3, 128, True), [10])["path"] == _ffi.KERNEL_PREFILL_BF16
+
+
+def test_causal_prompt_plans_pair_waves_and_skip_key_splits():
+    """Head_dim-64 causal prompts pair waves while the paired grid fits one
+    round of workgroup slots; causal prompts at head_dim 64/128 never take key
+    splits; chunks over longer caches keep single waves and key splits."""
+    p = plan_attention(KvAttentionConfig(1024, 32, 8, 64, True, 0), [0])
+    assert (p["block_waves"], p["splits"], p["workgroups"]) == (2, 1, 512)
+    assert (p["heads_per_block"], p["workgroup_queries"]) == (2, 32)
+    p = plan_attention(KvAttentionConfig(2048, 32, 8, 64, True, 0), [0])
+    assert (p["block_waves"], p["splits"], p["workgroups"]) == (1, 1, 512)
+    p = plan_attention(KvAttentionConfig(700, 24, 8, 64, True, 0), [0])
+    assert (p["block_waves"], p["heads_per_block"], p["workgroup_queries"]) == (2, 1, 64)
+    p = plan_attention(KvAttentionConfig(1024, 24, 8, 128, True, 0), [0])
+    assert (p["block_waves"], p["splits"]) == (1, 1)
+    p = plan_attention(KvAttentionConfig(100, 32, 8, 64, True, 0), [0])  # fewer than two tiles
+    assert p["block_waves"] == 1
+    p = plan_attention(KvAttentionConfig(128, 32, 8, 64, True, 0), [2048])
+    assert p["block_waves"] == 1 and p["splits"] > 1
+    p = plan_attention(KvAttentionConfig(1024, 32, 8, 64, False, 0), [0])
+    assert p["block_waves"] == 1
