@@ -87,6 +87,8 @@ def test_prefill_bf16_parity(gpu, name, S, P, Hq, Hkv, D, window):
     (333, 0, 16, 8),   # R = 2
     (700, 0, 24, 8),   # R = 3: one head, two query blocks per workgroup
     (129, 7, 8, 8),    # R = 1, a few cached keys, an odd tile count
+    (2048, 0, 4, 1),   # pairs with key splits (128 paired workgroups)
+    (1024, 0, 8, 2),   # pairs with key splits grouped by XCD
 ])
 def test_prefill_wave_pairs(gpu, S, P, Hq, Hkv):
     """Head_dim-64 causal prompts run wave pairs (two waves take alternate

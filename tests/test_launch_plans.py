@@ -226,6 +226,8 @@ BASELINE_PREFILL = [  # (name, S, P, Hq, Hkv, D, window, causal)
     ("pairs R=3 prompt 700", 700, 0, 24, 8, 64, 0, True),
     ("pairs R=1 prompt 129 after 7", 129, 7, 8, 8, 64, 0, True),
     ("llama-1B chunk 128 on 2048", 128, 2048, 32, 8, 64, 0, True),
+    ("llama-3B tp8 share prompt 4096", 4096, 0, 3, 1, 128, 0, True),
+    ("pairs with key splits, 4/1 heads 2048", 2048, 0, 4, 1, 64, 0, True),
 ]
 
 
@@ -341,6 +343,12 @@ def test_causal_prompt_plans_pair_waves_and_skip_key_splits():
     assert (p["block_waves"], p["heads_per_block"], p["workgroup_queries"]) == (2, 1, 64)
     p = plan_attention(KvAttentionConfig(1024, 24, 8, 128, True, 0), [0])
     assert (p["block_waves"], p["splits"]) == (1, 1)
+    # one GPU's share of a head split (3 query heads, 1 KV head): 32
+    # workgroups unsplit, so key splits still fill the GPU
+    p = plan_attention(KvAttentionConfig(4096, 3, 1, 128, True, 0), [0])
+    assert p["block_waves"] == 1 and p["splits"] > 1
+    p = plan_attention(KvAttentionConfig(2048, 4, 1, 64, True, 0), [0])  # 128 paired workgroups
+    assert p["block_waves"] == 2 and p["splits"] > 1
     p = plan_attention(KvAttentionConfig(100, 32, 8, 64, True, 0), [0])  # fewer than two tiles
     assert p["block_waves"] == 1
     p = plan_attention(KvAttentionConfig(128, 32, 8, 64, True, 0), [2048])
