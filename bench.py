@@ -1306,7 +1306,7 @@ def main() -> int:
             line[key] = {"phase": phase, **{k: round(v, 3) for k, v in res[key].items()}}
     if "prefill_attention_4096" in res:
         p = res["prefill_attention_4096"]
-        line["roofline_prefill"] = {"bound": "mfma", "kernel": "prefill_kernel<128,1,4,64,1> (the attention "
+        line["roofline_prefill"] = {"bound": "mfma", "kernel": "prefill_kernel<128,1,4,64,1,1> (the attention "
                                                                 "launch of prefill_attention_4096)",
                                     "achieved": round(p["TFLOPs"], 2), "peak": BF16_PEAK_TFLOPS,
                                     "unit": "TFLOP/s", "frac": round(p["TFLOPs"] / BF16_PEAK_TFLOPS, 4),
