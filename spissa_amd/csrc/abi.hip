@@ -1137,19 +1137,21 @@ static void plan_prefill(PrefillArgs &a, int D, int cus, PrefillPlan *p) {
   // 16384 keys measured 23.4 us with 4 splits against 25.1 us with 9). The
   // splits cover the widest tile range any workgroup has, so every
   // workgroup's keys are covered.
-  // Causal head_dim-64/128 prompts (fewer cached keys than queries) whose
-  // grid fills more than a quarter of the slots run unsplit: their partials
-  // are as large as the output, and writing and merging them cost more than
-  // the idle slots (reference-order call per layer: Llama-3.2-1B 1024-token
-  // prompt 33.2 us with 2 splits against 24.2 unsplit, 512 tokens 19.2
-  // against 15.5; Llama-3.2-3B 1024 tokens 40.1 with 3 splits against 33.7
-  // unsplit). Smaller grids still split (4 query heads on 1 KV head, 2048
-  // tokens at head_dim 64, 128 paired workgroups: 26.5 us unsplit, 24.3 with
-  // 4 splits; one GPU's share of Llama-3.2-3B's heads, 96 workgroups, 6
-  // splits).
+  // Causal head_dim-64/128 prompts (fewer cached keys than queries) run
+  // unsplit unless their grid fills at most a quarter of the slots and their
+  // longest query blocks visit at least 32 tiles: their partials are as large
+  // as the output, and writing and merging them cost more than short chains
+  // or a few idle slots save (reference-order call per layer: Llama-3.2-1B
+  // 1024-token prompt 33.2 us with 2 splits against 24.2 unsplit, 512 tokens
+  // 19.2 against 15.5; Llama-3.2-3B 512 / 1024 / 2048 tokens 27.9 / 40.1 /
+  // 67.9 split against 21.9 / 33.7 / 57.9 unsplit). Long chains on small
+  // grids still split (one GPU's share of Llama-3.2-3B's heads, 96
+  // workgroups of 64 tiles: 45.2 us with 6 splits against 77.2 unsplit; 4
+  // query heads on 1 KV head, 2048 tokens at head_dim 64, 128 paired
+  // workgroups: 24.1 with 4 splits against 26.5).
   const long base = prefill_base_workgroups(a, D);
-  const bool full_prompt = a.causal && a.P < a.S && D < 256 && 4 * base > slots;
   p->tiles = prefill_max_tile_span(a, D);
+  const bool full_prompt = a.causal && a.P < a.S && D < 256 && (4 * base > slots || p->tiles < 32);
   if (base < slots && !full_prompt) {
     const long min_tiles = D >= 256 && a.window > 0 ? 8 : 4;
     const long want = std::min(std::min((slots + base - 1) / base, p->tiles / min_tiles), (long)D);

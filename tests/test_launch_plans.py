@@ -343,6 +343,8 @@ def test_causal_prompt_plans_pair_waves_and_skip_key_splits():
     assert (p["block_waves"], p["heads_per_block"], p["workgroup_queries"]) == (2, 1, 64)
     p = plan_attention(KvAttentionConfig(1024, 24, 8, 128, True, 0), [0])
     assert (p["block_waves"], p["splits"]) == (1, 1)
+    p = plan_attention(KvAttentionConfig(512, 24, 8, 128, True, 0), [0])  # 96 workgroups of 8 tiles
+    assert (p["block_waves"], p["splits"]) == (1, 1)
     # one GPU's share of a head split (3 query heads, 1 KV head): 32
     # workgroups unsplit, so key splits still fill the GPU
     p = plan_attention(KvAttentionConfig(4096, 3, 1, 128, True, 0), [0])
