@@ -1136,7 +1136,11 @@ static void plan_prefill(PrefillArgs &a, int D, int cus, PrefillPlan *p) {
   // for windowed head_dim-256 layers: Gemma-3-4B's W1024 chunk of 128 on
   // 16384 keys measured 23.4 us with 4 splits against 25.1 us with 9). The
   // splits cover the widest tile range any workgroup has, so every
-  // workgroup's keys are covered.
+  // workgroup's keys are covered. Head_dim-64/128 chunks (at least as many
+  // cached keys as queries, so every block sees a similar range) aim at three
+  // quarters of a round: Llama-3.2-3B chunks of 256 on 8192 keys / 512 on
+  // 4096 / 64 on 8192 measured 55.5 / 58.2 / 34.2 us at 384 workgroups
+  // against 66.8 / 66.8 / 38.6 us at a full round.
   // Causal head_dim-64/128 prompts (fewer cached keys than queries) run
   // unsplit unless their grid fills at most a quarter of the slots and their
   // longest query blocks visit at least 32 tiles: their partials are as large
@@ -1154,7 +1158,8 @@ static void plan_prefill(PrefillArgs &a, int D, int cus, PrefillPlan *p) {
   const bool full_prompt = a.causal && a.P < a.S && D < 256 && (4 * base > slots || p->tiles < 32);
   if (base < slots && !full_prompt) {
     const long min_tiles = D >= 256 && a.window > 0 ? 8 : 4;
-    const long want = std::min(std::min((slots + base - 1) / base, p->tiles / min_tiles), (long)D);
+    const long target = a.P >= a.S && D < 256 ? slots * 3 / 4 : slots;
+    const long want = std::min(std::min((target + base - 1) / base, p->tiles / min_tiles), (long)D);
     if (want >= 2) {  // (at most head_dim splits: the measured useful range)
       a.tps = (int)((p->tiles + want - 1) / want);
       a.splits = (int)((p->tiles + a.tps - 1) / a.tps);

@@ -226,6 +226,8 @@ BASELINE_PREFILL = [  # (name, S, P, Hq, Hkv, D, window, causal)
     ("pairs R=3 prompt 700", 700, 0, 24, 8, 64, 0, True),
     ("pairs R=1 prompt 129 after 7", 129, 7, 8, 8, 64, 0, True),
     ("llama-1B chunk 128 on 2048", 128, 2048, 32, 8, 64, 0, True),
+    ("llama-3B chunk 256 on 8192", 256, 8192, 24, 8, 128, 0, True),
+    ("llama-3B chunk 64 on 8192", 64, 8192, 24, 8, 128, 0, True),
     ("llama-3B tp8 share prompt 4096", 4096, 0, 3, 1, 128, 0, True),
     ("pairs with key splits, 4/1 heads 2048", 2048, 0, 4, 1, 64, 0, True),
 ]
@@ -355,5 +357,10 @@ def test_causal_prompt_plans_pair_waves_and_skip_key_splits():
     assert p["block_waves"] == 1
     p = plan_attention(KvAttentionConfig(128, 32, 8, 64, True, 0), [2048])
     assert p["block_waves"] == 1 and p["splits"] > 1
+    # head_dim-64/128 chunks aim at three quarters of a round of slots
+    for S, P, want in ((256, 8192, 8), (512, 4096, 4), (64, 8192, 16)):
+        p = plan_attention(KvAttentionConfig(S, 24, 8, 128, True, 0), [P])
+        # (the split count is the tile range over whole tiles per split)
+        assert want - 1 <= p["splits"] <= want and p["workgroups"] <= 384, (S, P, p["splits"])
     p = plan_attention(KvAttentionConfig(1024, 32, 8, 64, False, 0), [0])
     assert p["block_waves"] == 1
