@@ -357,6 +357,9 @@ def test_causal_prompt_plans_pair_waves_and_skip_key_splits():
     assert p["block_waves"] == 1
     p = plan_attention(KvAttentionConfig(128, 32, 8, 64, True, 0), [2048])
     assert p["block_waves"] == 1 and p["splits"] > 1
+    # head_dim-256 causal prompts: one and a half rounds (Gemma-3-1B global)
+    p = plan_attention(KvAttentionConfig(4096, 4, 1, 256, True, 0), [0])
+    assert (p["splits"], p["workgroups"]) == (3, 768)
     # head_dim-64/128 chunks aim at three quarters of a round of slots
     for S, P, want in ((256, 8192, 8), (512, 4096, 4), (64, 8192, 16)):
         p = plan_attention(KvAttentionConfig(S, 24, 8, 128, True, 0), [P])
