@@ -971,14 +971,14 @@ static bool plan_decode(int D, int Hq, int Hkv, size_t window, const int *past, 
   const int R = Hq / Hkv;
   p->RB = pick_rb(R);
   p->HB = R / p->RB;
-  long total_rows = 0;
   int max_keys = 0;
+  int keys[kMaxDecodeBatch];  // (B <= kMaxDecodeBatch: one launch's sequences)
   for (int b = 0; b < B; ++b) {
     const int P = past[b];
     const int kstart = window > 0 ? std::max(0, P + 1 - (int)window) : 0;
     const int cached = P - kstart;  // visible cached keys; the new token is handled apart
     max_keys = std::max(max_keys, cached);
-    total_rows += (long)cached * Hkv * p->HB;
+    keys[b] = cached;
   }
   const size_t groups = (size_t)B * Hkv * p->HB;
   const size_t entry = (size_t)p->RB * (D + 2) * sizeof(float);
@@ -998,7 +998,7 @@ static bool plan_decode(int D, int Hq, int Hkv, size_t window, const int *past, 
     p->tok_split = fit >= 2 ? 1 : 0;
     split_cap = (int)std::min<size_t>(fit, kMaxDecodeSplits);
   }
-  p->kps = decode_keys_per_split(D, p->RB, total_rows, std::max(1, max_keys), split_cap - p->tok_split);
+  p->kps = decode_keys_per_split(D, p->RB, keys, B, (long)Hkv * p->HB, split_cap - p->tok_split);
   const int cached_splits = (max_keys + p->kps - 1) / p->kps;
   if (groups * (size_t)(cached_splits + 1) > (size_t)kDecodeGridWorkgroups) p->tok_split = 0;
   p->max_splits = p->tok_split ? cached_splits + 1 : std::max(1, cached_splits);

@@ -540,8 +540,21 @@ hipError_t launch_d(hipStream_t st, const DecodeArgs &a, int RB) {
 
 bool decode_supported(int D, int R) { return (D == 64 || D == 128 || D == 256) && R >= 1; }
 
-int decode_keys_per_split(int D, int RB, long total_rows, int max_keys, int split_cap) {
+int decode_keys_per_split(int D, int RB, const int *keys, int nseq, long heads, int split_cap) {
   const int chunk = 4 * (64 / (D / 8)) * rows_per_group(RB);  // keys of one workgroup iteration
+  long total_rows = 0;
+  int max_keys = 1;
+  for (int b = 0; b < nseq; ++b) {
+    total_rows += (long)keys[b] * heads;
+    max_keys = std::max(max_keys, keys[b]);
+  }
+  // Workgroups with work at kps keys per split (the others of the grid exit
+  // at once).
+  auto active = [&](long kps) {
+    long n = 0;
+    for (int b = 0; b < nseq; ++b) n += heads * ((keys[b] + kps - 1) / kps);
+    return n;
+  };
   // The fewest iterations per workgroup that keep the grid within
   // kDecodeGridWorkgroups, at the longest split that count allows: at a fixed
   // iteration count fewer workgroups ran faster (Llama-3.2-3B at 8192 keys,
@@ -550,6 +563,10 @@ int decode_keys_per_split(int D, int RB, long total_rows, int max_keys, int spli
   const long per = (total_rows + target - 1) / target;
   long kps = ((per + chunk - 1) / chunk) * chunk;
   if (kps < chunk) kps = chunk;
+  // Splits round up per sequence, which can take the workgroups with work past
+  // the target (batch 3 at 8192 keys: 24 groups x 22 splits = 528): whole
+  // iterations more per split until they fit.
+  while (active(kps) > target && kps < max_keys) kps += chunk;
   // Small layers (fewer keys per workgroup than one iteration's worth): one
   // row per lane group, so the grid has twice or three times the workgroups
   // (Llama-3.2-1B at 512 keys: 7.38 -> 6.99 us per layer), unless that takes

@@ -237,11 +237,11 @@ constexpr int kArgmaxMaxParts = 1024;  // partials one launch writes at most
 // n <= INT32_MAX - 1024.
 hipError_t launch_argmax(hipStream_t st, const float *x, int n, int excl, ArgmaxPart *parts, int *token);
 
-// Keys per split of a decode launch: total_rows = key rows summed over all
-// (sequence, KV head, head block) triples; max_keys = longest visible range;
-// the longest range gets at most split_cap splits (and never more than
-// kMaxDecodeSplits).
-int decode_keys_per_split(int D, int RB, long total_rows, int max_keys, int split_cap);
+// Keys per split of a decode launch: keys[b] = visible cached keys of
+// sequence b (nseq of them), heads = (KV head, head block) pairs per
+// sequence; the longest range gets at most split_cap splits (and never more
+// than kMaxDecodeSplits).
+int decode_keys_per_split(int D, int RB, const int *keys, int nseq, long heads, int split_cap);
 bool decode_supported(int D, int R);
 bool prefill_supported(int D);
 
