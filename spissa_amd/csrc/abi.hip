@@ -1440,14 +1440,27 @@ static int run_prefill_step(spissa_session *s, const spissa_rope_table *table, c
   PrefillPlan plan;
   plan_prefill_from_shadow(s, cfg, P, a, plan);
   ST_TRY(ensure_shadow(cache, s->stream));
-  ST_TRY(ensure_buf(s, s->qstage, S * cfg->num_heads * cfg->head_dim * sizeof(bf16)));
+  // Head_dim 64/128 without the QK-norm: the attention kernel rotates and
+  // scales the f32 q as it loads it (the same bf16 values), so the append
+  // pass stages no q (Llama-3.2-3B 4096-token step: the append pass moves 75
+  // MB less). The Gemma form and head_dim 256 stage the normed, rotated q in
+  // bf16.
+  const bool q_in_kernel = !norm && D <= 128;
+  bf16 *qb = nullptr;
+  if (!q_in_kernel) {
+    ST_TRY(ensure_buf(s, s->qstage, S * cfg->num_heads * cfg->head_dim * sizeof(bf16)));
+    qb = (bf16 *)s->qstage.p;
+  }
   if (plan.ppart_bytes) ST_TRY(ensure_buf(s, s->ppart, plan.ppart_bytes));
-  bf16 *qb = (bf16 *)s->qstage.p;
   PrefillNorm pn{};
   if (norm) pn = PrefillNorm{norm->q_norm, norm->k_norm, norm->eps, norm->q_prescale};
   HIP_TRY(launch_prefill_append(s->stream, d_q, d_k, d_v, table ? table->cos : nullptr, table ? table->sin : nullptr,
                                 P, S, cfg->kv_heads, cfg->num_heads, cfg->head_dim, cache->keys, cache->values,
                                 cache->kb, cache->vt, cache->shadow_cap, qb, a.qk_scale_log2, norm ? &pn : nullptr));
+  if (q_in_kernel && table) {
+    a.q_cos = table->cos;
+    a.q_sin = table->sin;
+  }
   ST_TRY(launch_prefill_from_shadow(s, a, cache, d_q, qb, d_out, D));
   cache->len = nl;
   return SPISSA_OK;

@@ -102,6 +102,10 @@ struct PrefillArgs {
   // Or, when set, Q already scaled by qk_scale_log2 and rounded to bf16
   // [S, Hq, D] (the fused prefill step's staging); q is then unused.
   const bf16 *qb;
+  // With q (f32): when set, the RoPE tables [position][D/2] q is rotated by
+  // at load, query i at position P + i (rotate-half, each product rounded
+  // apart, as the append pass rotates it), before the scale.
+  const float *q_cos, *q_sin;
   float *out;         // [S, Hq, D] f32
   // bf16 K/V for keys [0, P8) come from the cache shadow, keys [P8, P+S) from
   // the staging buffer; P8 is a multiple of kPrefillTileAlign, so no key tile
@@ -180,8 +184,9 @@ hipError_t launch_gemma_prologue(hipStream_t st, const float *cos_tab, const flo
                                  const float *kn, float eps, float prescale);
 // The append half of a fused prefill step: rows [0, S) of k/v (optionally
 // rotated with cos/sin rows at positions P + i) into cache rows [P, P + S)
-// and the bf16 shadow (zeros up to the next multiple of 64), and q rotated,
-// scaled by qscale and rounded into qb [S, Hq, D] bf16. D % 64 == 0.
+// and the bf16 shadow (zeros up to the next multiple of 64), and, when qb is
+// set, q rotated, scaled by qscale and rounded into qb [S, Hq, D] bf16.
+// D % 64 == 0.
 // Fused Gemma QK-norm of the prefill step's append (null q_norm: none): q
 // and k rows are RMS-normed with the [D] weights before RoPE (the sum of
 // squares in index order, ops.rs:159-179), and q is multiplied by q_prescale

@@ -307,13 +307,39 @@ __global__ __launch_bounds__(RB *NPB *KSP * 64, 2) void prefill_kernel(const Pre
         continue;
       }
       const float *qp = a.q + ((long)pos * a.Hq + head) * D + 8 * hl;
+      float x[DT][8];
 #pragma unroll
       for (int t = 0; t < DT; ++t) {
-        const float4 x0 = *reinterpret_cast<const float4 *>(qp + 16 * t);
-        const float4 x1 = *reinterpret_cast<const float4 *>(qp + 16 * t + 4);
+        *reinterpret_cast<float4 *>(&x[t][0]) = *reinterpret_cast<const float4 *>(qp + 16 * t);
+        *reinterpret_cast<float4 *>(&x[t][4]) = *reinterpret_cast<const float4 *>(qp + 16 * t + 4);
+      }
+      if (a.q_cos) {
+        // Rotate-half pairs (d, d + D/2) sit in one lane: dims 16t + 8hl + j
+        // and 16(t + DT/2) + 8hl + j. Each product is rounded apart
+        // (rotary.rs:467-481), as the append pass computes it.
+#pragma clang fp contract(off)
+        const float *cp = a.q_cos + (long)(a.P + pos) * (D / 2) + 8 * hl;
+        const float *sp = a.q_sin + (long)(a.P + pos) * (D / 2) + 8 * hl;
+#pragma unroll
+        for (int t = 0; t < DT / 2; ++t) {
+          float cs[8], sn[8];
+          *reinterpret_cast<float4 *>(&cs[0]) = *reinterpret_cast<const float4 *>(cp + 16 * t);
+          *reinterpret_cast<float4 *>(&cs[4]) = *reinterpret_cast<const float4 *>(cp + 16 * t + 4);
+          *reinterpret_cast<float4 *>(&sn[0]) = *reinterpret_cast<const float4 *>(sp + 16 * t);
+          *reinterpret_cast<float4 *>(&sn[4]) = *reinterpret_cast<const float4 *>(sp + 16 * t + 4);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float first = x[t][j], second = x[t + DT / 2][j];
+            x[t][j] = first * cs[j] - second * sn[j];
+            x[t + DT / 2][j] = second * cs[j] + first * sn[j];
+          }
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
         bf16x8 v;
-        v[0] = (bf16)(x0.x * c); v[1] = (bf16)(x0.y * c); v[2] = (bf16)(x0.z * c); v[3] = (bf16)(x0.w * c);
-        v[4] = (bf16)(x1.x * c); v[5] = (bf16)(x1.y * c); v[6] = (bf16)(x1.z * c); v[7] = (bf16)(x1.w * c);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = (bf16)(x[t][j] * c);
         qf[qb][t] = v;
       }
     }

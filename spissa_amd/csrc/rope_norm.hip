@@ -521,8 +521,9 @@ hipError_t launch_prefill_append(hipStream_t st, const float *q, const float *k,
   if (S == 0) return hipSuccess;
   const long pad_end = ((long)(P + S) + 63) & ~63L;
   if (D % 64 != 0 || cap % 64 != 0 || pad_end > (long)cap) return hipErrorInvalidValue;
-  const long kv_blocks = (pad_end - ((long)P & ~63L)) / 64, q_blocks = ((long)S + 63) / 64;
-  dim3 grid((unsigned)std::max(kv_blocks, q_blocks), (unsigned)(H + Hq), (unsigned)(D / 64));
+  const long kv_blocks = (pad_end - ((long)P & ~63L)) / 64, q_blocks = qb ? ((long)S + 63) / 64 : 0;
+  // (No qb: the attention rotates and scales q itself; only the K/V rows.)
+  dim3 grid((unsigned)std::max(kv_blocks, q_blocks), (unsigned)(H + (qb ? Hq : 0)), (unsigned)(D / 64));
   const PrefillNorm none{};
   auto kern = prefill_append_kernel<0>;
   if (norm) {
