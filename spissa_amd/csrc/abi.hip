@@ -1730,11 +1730,15 @@ static int linear_launch(spissa_session *s, const spissa_linear_weight *w, const
 // Several weights applied to the same input (the q, k and v projections):
 // one GEMV launch when all take the GEMV on an aligned input, else one
 // launch each. Results equal those of separate linear_launch calls.
+// norm_w (optional; every weight must take the GEMV): the input RMSNorm
+// folded into the projections.
 static int linear_launch_multi(spissa_session *s, const spissa_linear_weight *const *w, const float *d_x,
-                               size_t batch, float *const *d_out, int n) {
+                               size_t batch, float *const *d_out, int n, const float *norm_w = nullptr,
+                               float norm_eps = 0.0f) {
   if (batch == 0) return SPISSA_OK;
   if (batch > INT32_MAX) return set_err(SPISSA_ERR_SHAPE, "batch %zu too large", batch);
   if (reinterpret_cast<uintptr_t>(d_x) & 15) {
+    if (norm_w) return set_err(SPISSA_ERR_ARGUMENT, "the folded input norm needs a 16-byte aligned input");
     for (int i = 0; i < n; ++i) ST_TRY(linear_launch(s, w[i], d_x, nullptr, batch, d_out[i]));
     return SPISSA_OK;
   }
@@ -1749,6 +1753,8 @@ static int linear_launch_multi(spissa_session *s, const spissa_linear_weight *co
     a[i].N = (int)w[i]->out_features;
     a[i].K = (int)w[i]->in_features;
     a[i].dtype = w[i]->dtype;
+    a[i].norm_w = norm_w;
+    a[i].norm_eps = norm_eps;
   }
   HIP_TRY(hipSetDevice(s->device));
   HIP_TRY(launch_linear_multi(s->stream, a, n));
@@ -1951,15 +1957,26 @@ extern "C" int spissa_attention_sublayer_device(spissa_session *s, const spissa_
   }
   HIP_TRY(hipSetDevice(s->device));
   const float *xn = d_x;
+  // At up to four tokens every projection is a GEMV that reads each x row
+  // whole: the input RMSNorm folds into it (its launch saved) when the three
+  // weights share the GEMV path and the input is 16-byte aligned.
+  const float *fold = nullptr;
   if (L->d_input_norm) {
-    HIP_TRY(launch_rms_norm_tree(s->stream, d_x, L->d_input_norm, S, H, L->eps, r[0]));
-    xn = r[0];
+    bool gemv = S <= 4 && (reinterpret_cast<uintptr_t>(d_x) & 15) == 0;
+    for (const spissa_linear_weight *w : {L->q_weight, L->k_weight, L->v_weight})
+      gemv = gemv && w->dtype == L->q_weight->dtype && linear_path(w->dtype, (long)S, (long)H) == kLinearGemv;
+    if (gemv) {
+      fold = L->d_input_norm;
+    } else {
+      HIP_TRY(launch_rms_norm_tree(s->stream, d_x, L->d_input_norm, S, H, L->eps, r[0]));
+      xn = r[0];
+    }
   }
   float *q = r[1], *k = r[2], *v = r[3], *att = r[4];
   {
     const spissa_linear_weight *const wqkv[3] = {L->q_weight, L->k_weight, L->v_weight};
     float *const oqkv[3] = {q, k, v};
-    ST_TRY(linear_launch_multi(s, wqkv, xn, S, oqkv, 3));
+    ST_TRY(linear_launch_multi(s, wqkv, xn, S, oqkv, 3, fold, L->eps));
   }
   if (S == 1 && cache && decode_supported((int)D, (int)(Hq / Hkv)) && decode_cache_fits(cache)) {
     // (QK-norm,) RoPE, attention and append in the fused decode step

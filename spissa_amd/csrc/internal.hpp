@@ -94,6 +94,11 @@ struct LinearArgs {
   float *out;          // [M, N]
   int M, N, K;
   int dtype;           // spissa_dtype
+  // GEMV path only: when set, each x row is RMS-normed with these [K]
+  // weights first (ops.rs:159-179 up to rounding: the sum of squares rides
+  // the dot-product loop and 1/rms scales the finished sums).
+  const float *norm_w;
+  float norm_eps;
 };
 enum { kLinearGemv = 0, kLinearGemm = 1, kLinearGeneric = 2, kLinearSkinny = 3 };
 

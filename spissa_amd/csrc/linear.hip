@@ -112,11 +112,14 @@ __device__ __forceinline__ void gemv_rows(const LinearArgs &a, int block) {
 #pragma unroll
   for (int i = 0; i < RW; ++i) roff[i] = (long)min(r0 + i, a.N - 1) * a.K * (long)sizeof(WT);
 
-  float acc[RW][NB];
+  float acc[RW][NB], ss[NB];
 #pragma unroll
-  for (int i = 0; i < RW; ++i)
+  for (int t = 0; t < NB; ++t) {
+    ss[t] = 0.0f;
 #pragma unroll
-    for (int t = 0; t < NB; ++t) acc[i][t] = 0.0f;
+    for (int i = 0; i < RW; ++i) acc[i][t] = 0.0f;
+  }
+  const float *nw = a.norm_w;  // (uniform)
 
 #pragma unroll 2
   for (int c = lane; c < nch; c += 64) {
@@ -141,6 +144,18 @@ __device__ __forceinline__ void gemv_rows(const LinearArgs &a, int block) {
         xv[t][j + 3] = v.w;
       }
     }
+    if (nw) {  // folded RMSNorm: sum of squares, then x * w
+      float g[EPC];
+#pragma unroll
+      for (int j = 0; j < EPC; j += 4) *reinterpret_cast<float4 *>(&g[j]) = *reinterpret_cast<const float4 *>(nw + (long)c * EPC + j);
+#pragma unroll
+      for (int t = 0; t < NB; ++t)
+#pragma unroll
+        for (int j = 0; j < EPC; ++j) {
+          ss[t] = fmaf(xv[t][j], xv[t][j], ss[t]);
+          xv[t][j] *= g[j];
+        }
+    }
 #pragma unroll
     for (int i = 0; i < RW; ++i) {
       float wf[EPC];
@@ -155,6 +170,14 @@ __device__ __forceinline__ void gemv_rows(const LinearArgs &a, int block) {
   for (int i = 0; i < RW; ++i)
 #pragma unroll
     for (int t = 0; t < NB; ++t) acc[i][t] = wave_sum(acc[i][t]);
+  if (nw) {
+#pragma unroll
+    for (int t = 0; t < NB; ++t) {
+      const float inv = 1.0f / sqrtf(wave_sum(ss[t]) / (float)a.K + a.norm_eps);
+#pragma unroll
+      for (int i = 0; i < RW; ++i) acc[i][t] *= inv;
+    }
+  }
   if (lane < RW * NB) {
     const int i = lane / NB, t = lane % NB;
     const int r = r0 + i;
@@ -547,6 +570,7 @@ hipError_t launch_linear_multi(hipStream_t st, const LinearArgs *segs, int n) {
 
 hipError_t launch_linear(hipStream_t st, const LinearArgs &a, int path) {
   if (a.M <= 0 || a.N <= 0) return hipSuccess;
+  if (a.norm_w && path != kLinearGemv) return hipErrorInvalidValue;  // the folded norm is the GEMV's
   if (path == kLinearSkinny) {
     if (a.dtype != SPISSA_DTYPE_BF16 || a.K % 128 != 0 || a.M > 64) return hipErrorInvalidValue;
     const dim3 grid((unsigned)((a.N + kSkinnyRows - 1) / kSkinnyRows));
