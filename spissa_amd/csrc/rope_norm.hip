@@ -312,201 +312,204 @@ __global__ __launch_bounds__(256) void stage_bf16_kernel(const float *__restrict
 // The append and operand staging of a fused prefill step, in one pass over
 // the chunk's rows: the RoPE of rotary.rs:75-125 / 137-186 (optional, table
 // rows are absolute positions), then KvCache::append (rotary.rs:226-256).
-//   K/V blocks (blockIdx.y < H): cache position P + i receives row i of the
-//     chunk: the rotated key and the value in the f32 rows, the bf16 key in
-//     the shadow K [H, cap, D] and the bf16 value at slot vt_key_slot(pos) of
-//     the shadow V^T [H, D, cap]; shadow positions [P + S, pad_end) are zeroed
-//     so the last key tile the prefill kernel reads is finite.
-//   Q blocks (blockIdx.y >= H): query row i, rotated at position P + i,
+// Each quad of lanes owns one whole row of D floats; workgroups take RPW
+// rows of one tensor and head:
+//   K blocks (blockIdx.y < H): cache position P + i receives the rotated key
+//     row i of the chunk in the f32 rows and in bf16 in the shadow K
+//     [H, cap, D]; shadow positions [P + S, pad_end) are zeroed so the last
+//     key tile the prefill kernel reads is finite.
+//   V blocks (H <= blockIdx.y < 2H): the value row in the f32 rows, and in
+//     bf16 at slot vt_key_slot(pos) of the shadow V^T [H, D, cap] (through
+//     an LDS tile), zeros for the padding positions.
+//   Q blocks (blockIdx.y >= 2H): query row i, rotated at position P + i,
 //     times qscale, rounded to bf16 into qb [S, Hq, D] -- the prefill
 //     kernel's Q operand, the same bits it would form from the rotated f32 row.
-// 1 / sqrt(mean(x^2) + eps) of a row of D floats held by a quad of lanes
-// (lane c of the quad holds dims 32z + 8c + [0, 8) and D/2 + 32z + 8c + [0, 8)
-// for every z), with the sum of squares taken in index order as
-// ops.rs:159-179 takes it: the running sum visits the lanes in dim order,
-// eight rounded squares at a time, passed on with a quad rotation (DPP).
+// Lane c of a quad holds dims 32z + 16e + 4c + [0, 4) of each half (z < D/64,
+// e < 2): the quad covers 64 contiguous bytes of a row per access, and rotary
+// pair p = (p, D/2 + p) sits in one lane.
+// With NORM the Gemma QK-norm (ops.rs:159-179, as models/gemma/generate.rs:
+// 232-245 calls it) comes first: the row's sum of squares in index order,
+// four rounded squares at a time, the running sum passed from lane to lane
+// of the quad by a DPP rotation; then x * inv * w.
+// Grid: (position blocks of RPW, 2H + Hq (Hq only with qb)), 4 * RPW threads.
 template <int D>
-__device__ __forceinline__ float quad_inv_rms(const float *row, int c, float eps) {
+__device__ __forceinline__ float quad_inv_rms(const float4 (&x)[2][D / 64][2], int c, float eps) {
 #pragma clang fp contract(off)
-  constexpr int HALF = D / 2, G = HALF / 32;
-  float4 x[2][G][2];
-#pragma unroll
-  for (int part = 0; part < 2; ++part)
-#pragma unroll
-    for (int z = 0; z < G; ++z) {
-      x[part][z][0] = *reinterpret_cast<const float4 *>(row + part * HALF + 32 * z + 8 * c);
-      x[part][z][1] = *reinterpret_cast<const float4 *>(row + part * HALF + 32 * z + 8 * c + 4);
-    }
+  constexpr int G = D / 64;
   float acc = 0.0f;
 #pragma unroll
   for (int part = 0; part < 2; ++part)
 #pragma unroll
-    for (int z = 0; z < G; ++z) {
-      const float *v = reinterpret_cast<const float *>(x[part][z]);
+    for (int z = 0; z < G; ++z)
 #pragma unroll
-      for (int turn = 0; turn < 4; ++turn) {
-        float t = acc;
+      for (int e = 0; e < 2; ++e) {
+        const float *v = reinterpret_cast<const float *>(&x[part][z][e]);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) t = t + v[j] * v[j];
-        acc = c == turn ? t : acc;
-        // lane c takes lane c - 1's sum (quad_perm [3, 0, 1, 2])
-        acc = __builtin_amdgcn_update_dpp(acc, acc, 0x93, 0xf, 0xf, false);
+        for (int turn = 0; turn < 4; ++turn) {
+          float t = acc;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) t = t + v[j] * v[j];
+          acc = c == turn ? t : acc;
+          // lane c takes lane c - 1's sum (quad_perm [3, 0, 1, 2])
+          acc = __builtin_amdgcn_update_dpp(acc, acc, 0x93, 0xf, 0xf, false);
+        }
       }
-    }
   // lane 0 of the quad holds the total; every lane takes it (quad_perm [0, 0, 0, 0])
   acc = __builtin_amdgcn_update_dpp(acc, acc, 0x00, 0xf, 0xf, false);
   const float mean_square = acc / (float)D;
   return 1.0f / sqrtf(mean_square + eps);
 }
 
-// A block owns 64 positions and the 32 rotary pairs [32z, 32z + 32) of one
-// head, i.e. dims [32z, +32) and [D/2 + 32z, +32); thread t holds position
-// t / 4 and the eight pairs 8(t % 4) .. +7 of that range: a float4 pair of
-// each half. Values pass through an LDS tile for the V^T stores.
-// Grid: (position blocks, H + Hq, D / 64), 256 threads. NORM_D: 0, or the
-// head dim with the Gemma QK-norm folded in (each quad of lanes first takes
-// its full row's 1/rms).
-template <int NORM_D>
-__global__ __launch_bounds__(256) void prefill_append_kernel(
+template <int D, bool NORM, int RPW>
+__global__ __launch_bounds__(RPW * 4) void prefill_append_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
-    const float *__restrict__ cos_tab, const float *__restrict__ sin_tab, long P, long S, int H, int Hq, int D,
+    const float *__restrict__ cos_tab, const float *__restrict__ sin_tab, long P, long S, int H, int Hq,
     float *__restrict__ cache_k, float *__restrict__ cache_v, bf16 *__restrict__ kb, bf16 *__restrict__ vt,
     long cap, long pad_end, bf16 *__restrict__ qb, float qscale, const PrefillNorm nrm) {
 #pragma clang fp contract(off)
   typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
-  __shared__ float tile[64][65];  // V[position][lo 32 | hi 32 dims], padded against bank conflicts
-  const int half = D / 2;
+  typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+  constexpr int HALF = D / 2, G = D / 64;
+  __shared__ bf16 tile[RPW][D + 8];  // V[position][dim] of the block, padded
   const int r = threadIdx.x >> 2, c = threadIdx.x & 3;
-  const int p0 = 32 * blockIdx.z + 8 * c;  // first pair of this thread
-  const bool kv = (int)blockIdx.y < H;
-
-  auto rotate = [&](float4 (&lo)[2], float4 (&hi)[2], long pos) {
-    if (!cos_tab) return;
-    const float *cp = cos_tab + pos * half + p0, *sp = sin_tab + pos * half + p0;
-    float *a = reinterpret_cast<float *>(lo), *b = reinterpret_cast<float *>(hi);
-    float cs[8], sn[8];
-    *reinterpret_cast<float4 *>(cs) = *reinterpret_cast<const float4 *>(cp);
-    *reinterpret_cast<float4 *>(cs + 4) = *reinterpret_cast<const float4 *>(cp + 4);
-    *reinterpret_cast<float4 *>(sn) = *reinterpret_cast<const float4 *>(sp);
-    *reinterpret_cast<float4 *>(sn + 4) = *reinterpret_cast<const float4 *>(sp + 4);
+  float4 x[2][G][2];  // [half][z][e]
+  auto off = [&](int z, int e) { return 32 * z + 16 * e + 4 * c; };
+  auto load_row = [&](const float *row) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {  // rotate_neox_pair (rotary.rs:467-481)
-      const float first = a[j], second = b[j];
-      a[j] = first * cs[j] - second * sn[j];
-      b[j] = second * cs[j] + first * sn[j];
-    }
-  };
-  auto to_bf16 = [](const float4 (&x)[2], float s) {
-    const float *f = reinterpret_cast<const float *>(x);
-    bf16x8 o;
+    for (int part = 0; part < 2; ++part)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] = (bf16)(f[j] * s);
-    return o;
-  };
-  auto load2 = [](const float *p, float4 (&x)[2]) {
-    x[0] = *reinterpret_cast<const float4 *>(p);
-    x[1] = *reinterpret_cast<const float4 *>(p + 4);
-  };
-  auto store2 = [](float *p, const float4 (&x)[2]) {
-    *reinterpret_cast<float4 *>(p) = x[0];
-    *reinterpret_cast<float4 *>(p + 4) = x[1];
-  };
-  auto row_inv = [&](const float *row) {
-    if constexpr (NORM_D > 0) return quad_inv_rms<NORM_D>(row, c, nrm.eps);
-    return 1.0f;
-  };
-  // Gemma QK-norm of a row's eight pairs: (x * inv) * w, as the prologue.
-  auto norm = [&](float4 (&lo)[2], float4 (&hi)[2], float inv, const float *w) {
-    float4 wl[2], wh[2];
-    load2(w + p0, wl);
-    load2(w + half + p0, wh);
-    float *a = reinterpret_cast<float *>(lo), *b = reinterpret_cast<float *>(hi);
-    const float *x = reinterpret_cast<const float *>(wl), *y = reinterpret_cast<const float *>(wh);
+      for (int z = 0; z < G; ++z)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      a[j] = a[j] * inv * x[j];
-      b[j] = b[j] * inv * y[j];
-    }
+        for (int e = 0; e < 2; ++e) x[part][z][e] = *reinterpret_cast<const float4 *>(row + part * HALF + off(z, e));
   };
-
-  if (!kv) {
-    const int hq = blockIdx.y - H;
-    const long i = 64L * blockIdx.x + r;
-    if (i >= S) return;
-    const float *src = q + (i * Hq + hq) * (long)D;
-    float4 lo[2], hi[2];
-    load2(src + p0, lo);
-    load2(src + half + p0, hi);
-    if (NORM_D) norm(lo, hi, row_inv(src), nrm.q_norm);
-    rotate(lo, hi, P + i);
-    if (NORM_D) {
+  auto load8 = [&](const float *p, int z, float (&o)[8]) {
+    *reinterpret_cast<float4 *>(o) = *reinterpret_cast<const float4 *>(p + off(z, 0));
+    *reinterpret_cast<float4 *>(o + 4) = *reinterpret_cast<const float4 *>(p + off(z, 1));
+  };
+  // QK-norm (with NORM) and rotate_neox_pair (rotary.rs:467-481) at `pos`.
+  auto norm_rotate = [&](const float *w, long pos) {
+    float inv = 1.0f;
+    if constexpr (NORM) inv = quad_inv_rms<D>(x, c, nrm.eps);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        lo[j] = make_float4(lo[j].x * nrm.q_prescale, lo[j].y * nrm.q_prescale, lo[j].z * nrm.q_prescale,
-                            lo[j].w * nrm.q_prescale);
-        hi[j] = make_float4(hi[j].x * nrm.q_prescale, hi[j].y * nrm.q_prescale, hi[j].z * nrm.q_prescale,
-                            hi[j].w * nrm.q_prescale);
+    for (int z = 0; z < G; ++z) {
+      float *a = reinterpret_cast<float *>(x[0][z]), *b = reinterpret_cast<float *>(x[1][z]);
+      if constexpr (NORM) {
+        float wl[8], wh[8];
+        load8(w, z, wl);
+        load8(w + HALF, z, wh);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          a[j] = a[j] * inv * wl[j];
+          b[j] = b[j] * inv * wh[j];
+        }
+      }
+      if (cos_tab) {
+        float cs[8], sn[8];
+        load8(cos_tab + pos * HALF, z, cs);
+        load8(sin_tab + pos * HALF, z, sn);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float first = a[j], second = b[j];
+          a[j] = first * cs[j] - second * sn[j];
+          b[j] = second * cs[j] + first * sn[j];
+        }
       }
     }
-    bf16 *dst = qb + (i * Hq + hq) * (long)D;
-    *reinterpret_cast<bf16x8 *>(dst + p0) = to_bf16(lo, qscale);
-    *reinterpret_cast<bf16x8 *>(dst + half + p0) = to_bf16(hi, qscale);
+  };
+  auto store_bf16 = [&](bf16 *dst, float s) {
+#pragma unroll
+    for (int part = 0; part < 2; ++part)
+#pragma unroll
+      for (int z = 0; z < G; ++z)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const float4 f = x[part][z][e];
+          bf16x4 o;
+          o[0] = (bf16)(f.x * s); o[1] = (bf16)(f.y * s); o[2] = (bf16)(f.z * s); o[3] = (bf16)(f.w * s);
+          *reinterpret_cast<bf16x4 *>(dst + part * HALF + off(z, e)) = o;
+        }
+  };
+  auto store_f32 = [&](float *dst) {
+#pragma unroll
+    for (int part = 0; part < 2; ++part)
+#pragma unroll
+      for (int z = 0; z < G; ++z)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) *reinterpret_cast<float4 *>(dst + part * HALF + off(z, e)) = x[part][z][e];
+  };
+
+  const int y = blockIdx.y;
+  if (y >= 2 * H) {
+    const int hq = y - 2 * H;
+    const long i = (long)RPW * blockIdx.x + r;
+    if (i >= S) return;
+    load_row(q + (i * Hq + hq) * (long)D);
+    norm_rotate(nrm.q_norm, P + i);
+    if constexpr (NORM) {
+#pragma unroll
+      for (int part = 0; part < 2; ++part)
+#pragma unroll
+        for (int z = 0; z < G; ++z)
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            float4 &t = x[part][z][e];
+            t = make_float4(t.x * nrm.q_prescale, t.y * nrm.q_prescale, t.z * nrm.q_prescale, t.w * nrm.q_prescale);
+          }
+    }
+    store_bf16(qb + (i * Hq + hq) * (long)D, qscale);
     return;
   }
-
-  const int h = blockIdx.y;
-  const long P0 = (P & ~63L) + 64L * blockIdx.x;
+  const bool is_k = y < H;
+  const int h = is_k ? y : y - H;
+  const long P0 = (P & ~(long)(RPW - 1)) + (long)RPW * blockIdx.x;
   const long pos = P0 + r;
-  float4 klo[2], khi[2], vlo[2], vhi[2];
-  const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-  klo[0] = klo[1] = khi[0] = khi[1] = vlo[0] = vlo[1] = vhi[0] = vhi[1] = z;
   const bool row = pos >= P && pos < P + S;
   if (row) {
-    const long i = pos - P;
-    const float *ks = k + (i * H + h) * (long)D, *vs = v + (i * H + h) * (long)D;
-    load2(ks + p0, klo);
-    load2(ks + half + p0, khi);
-    load2(vs + p0, vlo);
-    load2(vs + half + p0, vhi);
-    if (NORM_D) norm(klo, khi, row_inv(ks), nrm.k_norm);
-    rotate(klo, khi, pos);
-    float *ck = cache_k + (pos * H + h) * (long)D, *cv = cache_v + (pos * H + h) * (long)D;
-    store2(ck + p0, klo);
-    store2(ck + half + p0, khi);
-    store2(cv + p0, vlo);
-    store2(cv + half + p0, vhi);
-  }
-  if (pos >= P && pos < pad_end) {  // the chunk's rows, then zero padding
-    bf16 *dk = kb + ((long)h * cap + pos) * D;
-    *reinterpret_cast<bf16x8 *>(dk + p0) = to_bf16(klo, 1.0f);
-    *reinterpret_cast<bf16x8 *>(dk + half + p0) = to_bf16(khi, 1.0f);
-  }
-  {
-    float *t = &tile[r][8 * c];
-    const float *a = reinterpret_cast<const float *>(vlo), *b = reinterpret_cast<const float *>(vhi);
+    load_row((is_k ? k : v) + ((pos - P) * H + h) * (long)D);
+  } else {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      t[j] = a[j];
-      t[32 + j] = b[j];
-    }
+    for (int part = 0; part < 2; ++part)
+#pragma unroll
+      for (int z = 0; z < G; ++z) x[part][z][0] = x[part][z][1] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
+  if (is_k) {
+    if (row) {
+      norm_rotate(nrm.k_norm, pos);
+      store_f32(cache_k + (pos * H + h) * (long)D);
+    }
+    if (pos >= P && pos < pad_end) store_bf16(kb + ((long)h * cap + pos) * D, 1.0f);  // the rows, then zeros
+    return;
+  }
+  if (row) store_f32(cache_v + (pos * H + h) * (long)D);
+#pragma unroll
+  for (int part = 0; part < 2; ++part)
+#pragma unroll
+    for (int z = 0; z < G; ++z)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float4 f = x[part][z][e];
+        bf16x4 o;
+        o[0] = (bf16)f.x; o[1] = (bf16)f.y; o[2] = (bf16)f.z; o[3] = (bf16)f.w;
+        *reinterpret_cast<bf16x4 *>(&tile[r][part * HALF + off(z, e)]) = o;
+      }
   __syncthreads();
-  // V^T: 64 dim rows (lo 32, hi 32) x 64 slots, eight slots per store.
-  for (int w = threadIdx.x; w < 64 * 8; w += 256) {
-    const int dd = w >> 3, c8 = w & 7;
-    const int dim = dd < 32 ? 32 * blockIdx.z + dd : half + 32 * blockIdx.z + (dd - 32);
+  // V^T: D dim rows x RPW slots, eight slots per store; slot s holds the key
+  // at position vt_key_slot(s), which lies in the same aligned 16-group.
+  constexpr int SG = RPW / 8;
+  for (int w = threadIdx.x; w < D * SG; w += RPW * 4) {
+    const int dd = w / SG, c8 = w % SG;
     const long s0 = P0 + 8 * c8;
-    bf16 *dst = vt + ((long)h * D + dim) * cap;
+    bf16 *dst = vt + ((long)h * D + dd) * cap;
     const long g0 = s0 & ~15L;  // the aligned 16-key group these slots hold
     if (g0 >= P && g0 + 16 <= pad_end) {
       bf16x8 vv;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) vv[j] = (bf16)tile[vt_key_slot(s0 + j) - P0][dd];
+      for (int j = 0; j < 8; ++j) vv[j] = tile[vt_key_slot(s0 + j) - P0][dd];
       *reinterpret_cast<bf16x8 *>(dst + s0) = vv;
     } else {
       for (int j = 0; j < 8; ++j) {
         const long sl = s0 + j, key = vt_key_slot(sl);
-        if (key >= P && key < pad_end) dst[sl] = (bf16)tile[key - P0][dd];
+        if (key >= P && key < pad_end) dst[sl] = tile[key - P0][dd];
       }
     }
   }
@@ -514,25 +517,54 @@ __global__ __launch_bounds__(256) void prefill_append_kernel(
 
 static inline unsigned blocks_for(long n, int per) { return (unsigned)((n + per - 1) / per); }
 
+template <int D, bool NORM, int RPW>
+static hipError_t launch_append_rows(hipStream_t st, const float *q, const float *k, const float *v,
+                                     const float *cos_tab, const float *sin_tab, long P, long S, int H, int Hq,
+                                     float *cache_k, float *cache_v, bf16 *kb, bf16 *vt, long cap, long pad_end,
+                                     bf16 *qb, float qscale, const PrefillNorm &nrm) {
+  const long kv_blocks = (pad_end - (P & ~(long)(RPW - 1))) / RPW, q_blocks = qb ? (S + RPW - 1) / RPW : 0;
+  dim3 grid((unsigned)std::max(kv_blocks, q_blocks), (unsigned)(2 * H + (qb ? Hq : 0)));
+  hipLaunchKernelGGL((prefill_append_kernel<D, NORM, RPW>), grid, dim3(4 * RPW), 0, st, q, k, v, cos_tab, sin_tab, P,
+                     S, H, Hq, cache_k, cache_v, kb, vt, cap, pad_end, qb, qscale, nrm);
+  return hipGetLastError();
+}
+
+template <int D, bool NORM>
+static hipError_t launch_append_d(hipStream_t st, const float *q, const float *k, const float *v,
+                                  const float *cos_tab, const float *sin_tab, long P, long S, int H, int Hq,
+                                  float *cache_k, float *cache_v, bf16 *kb, bf16 *vt, long cap, long pad_end,
+                                  bf16 *qb, float qscale, const PrefillNorm &nrm) {
+  // 64-row workgroups when they give every CU one (Llama-3.2-3B 4096 rows:
+  // 1024; Gemma-3-1B: 384), else 16-row ones (one wave each) for more
+  // workgroups on short chunks.
+  const long blocks64 = (pad_end - (P & ~63L)) / 64 * (2 * H + (qb ? Hq : 0));
+  if (blocks64 >= 256)
+    return launch_append_rows<D, NORM, 64>(st, q, k, v, cos_tab, sin_tab, P, S, H, Hq, cache_k, cache_v, kb, vt, cap,
+                                           pad_end, qb, qscale, nrm);
+  return launch_append_rows<D, NORM, 16>(st, q, k, v, cos_tab, sin_tab, P, S, H, Hq, cache_k, cache_v, kb, vt, cap,
+                                         pad_end, qb, qscale, nrm);
+}
+
 hipError_t launch_prefill_append(hipStream_t st, const float *q, const float *k, const float *v,
                                  const float *cos_tab, const float *sin_tab, size_t P, size_t S, size_t H,
                                  size_t Hq, size_t D, float *cache_k, float *cache_v, bf16 *kb, bf16 *vt,
                                  size_t cap, bf16 *qb, float qscale, const PrefillNorm *norm) {
   if (S == 0) return hipSuccess;
   const long pad_end = ((long)(P + S) + 63) & ~63L;
-  if (D % 64 != 0 || cap % 64 != 0 || pad_end > (long)cap) return hipErrorInvalidValue;
-  const long kv_blocks = (pad_end - ((long)P & ~63L)) / 64, q_blocks = qb ? ((long)S + 63) / 64 : 0;
+  if ((D != 64 && D != 128 && D != 256) || cap % 64 != 0 || pad_end > (long)cap) return hipErrorInvalidValue;
   // (No qb: the attention rotates and scales q itself; only the K/V rows.)
-  dim3 grid((unsigned)std::max(kv_blocks, q_blocks), (unsigned)(H + (qb ? Hq : 0)), (unsigned)(D / 64));
-  const PrefillNorm none{};
-  auto kern = prefill_append_kernel<0>;
-  if (norm) {
-    if (D != 64 && D != 128 && D != 256) return hipErrorInvalidValue;
-    kern = D == 64 ? prefill_append_kernel<64> : D == 128 ? prefill_append_kernel<128> : prefill_append_kernel<256>;
-  }
-  hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, q, k, v, cos_tab, sin_tab, (long)P, (long)S, (int)H, (int)Hq,
-                     (int)D, cache_k, cache_v, kb, vt, (long)cap, pad_end, qb, qscale, norm ? *norm : none);
-  return hipGetLastError();
+  const PrefillNorm nrm = norm ? *norm : PrefillNorm{};
+#define SPISSA_APPEND_D(DD)                                                                                          \
+  if (D == DD)                                                                                                       \
+    return norm ? launch_append_d<DD, true>(st, q, k, v, cos_tab, sin_tab, (long)P, (long)S, (int)H, (int)Hq, cache_k, \
+                                            cache_v, kb, vt, (long)cap, pad_end, qb, qscale, nrm)                    \
+                : launch_append_d<DD, false>(st, q, k, v, cos_tab, sin_tab, (long)P, (long)S, (int)H, (int)Hq, cache_k, \
+                                             cache_v, kb, vt, (long)cap, pad_end, qb, qscale, nrm);
+  SPISSA_APPEND_D(64)
+  SPISSA_APPEND_D(128)
+  SPISSA_APPEND_D(256)
+#undef SPISSA_APPEND_D
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_rope_apply(hipStream_t st, const float *cos_tab, const float *sin_tab,

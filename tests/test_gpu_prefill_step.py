@@ -48,6 +48,8 @@ CASES = [  # name, S, P, Hq, Hkv, D, window, rope kind, base, divisor
     ("gemma-4B local chunk 128 on 1000 W1024", 128, 1000, 8, 4, 256, 1024, "gemma", 10000.0, 1.0),
     ("gemma-1B global prefill 300, divisor 8", 300, 0, 4, 1, 256, 0, "gemma", 1000000.0, 8.0),
     ("no RoPE, two tokens", 2, 5, 8, 2, 64, 0, None, 0.0, 1.0),
+    # (64-row append workgroups: at least one per CU; the cases above take 16-row ones)
+    ("8/8 heads, chunk 1000 on unaligned 37", 1000, 37, 8, 8, 128, 0, "llama", 500000.0, 1.0),
 ]
 
 
@@ -194,6 +196,7 @@ GEMMA_CASES = [  # name, S, P, Hq, Hkv, D, window, base, divisor, query_pre_attn
     ("prescale != 1, chunk 77 on 129", 77, 129, 8, 4, 256, 0, 10000.0, 1.0, 224.0),
     ("head_dim 128, 65 rows", 65, 0, 8, 2, 128, 0, 10000.0, 1.0, 128.0),
     ("head_dim 64, chunk 130 on 7", 130, 7, 6, 2, 64, 0, 10000.0, 1.0, 64.0),
+    ("head_dim 64, 8/8 heads, chunk 700 on 37 (64-row append workgroups)", 700, 37, 8, 8, 64, 0, 10000.0, 1.0, 64.0),
 ]
 
 
