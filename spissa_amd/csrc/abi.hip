@@ -1719,6 +1719,7 @@ static int linear_launch(spissa_session *s, const spissa_linear_weight *w, const
   a.N = (int)w->out_features;
   a.K = (int)w->in_features;
   a.dtype = w->dtype;
+  a.cus = s->cus;
   int path = linear_path(a.dtype, a.M, a.K);
   // the vector kernels read 16-byte pieces of x and of the weight rows
   if (path != kLinearGeneric && (reinterpret_cast<uintptr_t>(d_x) & 15)) path = kLinearGeneric;
@@ -1755,6 +1756,7 @@ static int linear_launch_multi(spissa_session *s, const spissa_linear_weight *co
     a[i].dtype = w[i]->dtype;
     a[i].norm_w = norm_w;
     a[i].norm_eps = norm_eps;
+    a[i].cus = s->cus;
   }
   HIP_TRY(hipSetDevice(s->device));
   HIP_TRY(launch_linear_multi(s->stream, a, n));

@@ -99,6 +99,7 @@ struct LinearArgs {
   // the dot-product loop and 1/rms scales the finished sums).
   const float *norm_w;
   float norm_eps;
+  int cus;  // compute units of the device (sizes the GEMM's tiles; 0: 256)
 };
 enum { kLinearGemv = 0, kLinearGemm = 1, kLinearGeneric = 2, kLinearSkinny = 3 };
 

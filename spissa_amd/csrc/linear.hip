@@ -16,9 +16,9 @@
 //    decode): weight fragments straight from HBM into 16x16x32 MFMAs, the
 //    activations split as below, K split over the workgroup's four waves.
 //  - linear_gemm_kernel (bf16 weights, M > 64, K % 32 == 0: prefill): MFMA
-//    v_mfma_f32_32x32x16_bf16 on 128 x 256 output tiles, 32-deep k tiles in
-//    LDS (weights copied global -> LDS with global_load_lds_dwordx4,
-//    activations converted in registers), four waves per SIMD. Each f32 activation is split into
+//    v_mfma_f32_32x32x16_bf16 on 128 x 256 or 256 x 320 output tiles, 32-deep
+//    k tiles in LDS (weights copied global -> LDS with global_load_lds_dwordx4,
+//    activations converted in registers). Each f32 activation is split into
 //    bf16 hi = rne(x) and lo = rne(x - hi), and both halves meet the bf16
 //    weight: the products are exact in f32 and the residual of the split is
 //    below 2^-16 |x|, so the result carries f32-level error rather than bf16.
@@ -209,8 +209,8 @@ __global__ __launch_bounds__(256) void linear_gemv_multi_kernel(const LinearSegm
 }
 
 namespace {
-constexpr int kBM = 128, kBN = 256, kBK = 32;  // GEMM tiles
-constexpr int kRowBytes = kBK * 2;              // one bf16 tile row: 64 bytes, four 16-byte chunks
+constexpr int kBK = 32;              // GEMM k tile
+constexpr int kRowBytes = kBK * 2;  // one bf16 tile row: 64 bytes, four 16-byte chunks
 
 // Chunk swizzle of a 64-byte LDS row: any 8 aligned consecutive rows reading
 // the same chunk hit 8 distinct 16-byte groups modulo 128 bytes.
@@ -223,127 +223,172 @@ typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
 __device__ __forceinline__ unsigned bf16x2_rne(float a, float b) {
   return __builtin_bit_cast(unsigned, __builtin_convertvector((f32x2){a, b}, bf16x2));
 }
+
+// 16 bytes per lane global -> LDS (global_load_lds_dwordx4); the LDS address
+// is the wave's base, lane l's bytes land at +16 l.
+__device__ __forceinline__ void copy16_to_lds(const char *src, char *dst) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void *)dst, 16, 0, 0);
+}
+// s_waitcnt vmcnt(N) (N < 16; the other counters unconstrained).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+}
 }  // namespace
 
-// Grid: ceil(M / 128) * ceil(N / 256) workgroups of 512 threads (2 x 4 waves,
-// 64 x 64 outputs each). K % 32 == 0. Rows past M or N are read clamped and
-// not stored.
+// Grid: ceil(M / BM) * ceil(N / BN) workgroups of 512 threads (WM x WN waves,
+// each (BM / WM) x (BN / WN) outputs in 32 x 32 blocks). K % 32 == 0. Rows
+// past M or N are read clamped and not stored. Two tile shapes
+// (linear_gemm_shape picks one per call):
+//   128 x 256, 2 x 4 waves of 64 x 64: 64 KB of LDS and at most 128 VGPRs, so
+//     two workgroups share a CU (four waves per SIMD);
+//   256 x 320, 4 x 2 waves of 64 x 160: 104 KB of LDS, one workgroup per CU
+//     (two waves per SIMD), for grids whose 128 x 256 tiles would leave a
+//     second round of slots mostly empty.
 // Pipeline, per 32-deep k tile t: the weight tile is copied into one of two
 // LDS buffers one step ahead (issued in step t-1), and the activations are
 // loaded into registers two steps ahead (issued in step t-2, split and written
 // to one of two LDS buffers at the start of step t-1). Step t writes the
 // activations of tile t+1, copies the weights of tile t+1, loads the
-// activations of tile t+2, runs the 16 MFMAs of tile t per wave, then waits
-// for everything but the activation loads it just issued. 64 KB of LDS and
-// at most 128 VGPRs let two workgroups share a CU (four waves per SIMD).
-// Measured on the 4096 x 5120 x 3072 projection: 284 us; 128 x 128 tiles of
-// four waves took 292 us with this pipeline (three workgroups per CU) and
-// 342 us with a third weight buffer two steps ahead (two per CU).
-__global__ __launch_bounds__(512, 2) void linear_gemm_kernel(const LinearArgs a) {
-  __shared__ __attribute__((aligned(1024))) char w_lds0[kBN * kRowBytes];
-  __shared__ __attribute__((aligned(1024))) char w_lds1[kBN * kRowBytes];
-  __shared__ __attribute__((aligned(1024))) char xh_lds0[kBM * kRowBytes];
-  __shared__ __attribute__((aligned(1024))) char xh_lds1[kBM * kRowBytes];
-  __shared__ __attribute__((aligned(1024))) char xl_lds0[kBM * kRowBytes];
-  __shared__ __attribute__((aligned(1024))) char xl_lds1[kBM * kRowBytes];
+// activations of tile t+2, runs the MFMAs of tile t, then waits for
+// everything but the activation loads it just issued.
+// Measured on the 4096 x 5120 x 3072 projection: 284 us with 128 x 256 tiles,
+// 242-250 us with 256 x 320 ones (MFMA busy 53% under the profiler, no LDS
+// bank conflicts); 128 x 128 tiles of four waves took 292 us with this
+// pipeline (three workgroups per CU) and 342 us with a third weight buffer two
+// steps ahead (two per CU). Reading a step's first fragments before its
+// copies, and an XCD-grouped tile order (each XCD a 4 x 8 block of tiles:
+// 424 MB fetched beyond L2 for 81 MB of operands otherwise), measured within
+// noise.
+template <int BM, int BN, int WM, int WN, int MINWG>
+__global__ __launch_bounds__(WM * WN * 64, MINWG) void linear_gemm_kernel(const LinearArgs a) {
+  static_assert(WM * WN == 8, "eight waves");
+  constexpr int TM = BM / WM, TN = BN / WN;  // the wave's outputs
+  constexpr int BI = TM / 32, BJ = TN / 32;  // its 32 x 32 blocks
+  static_assert(BI * 32 == TM && BJ * 32 == TN, "32 x 32 blocks");
+  constexpr int WCOPIES = BN * kRowBytes / 1024;  // 1 KB weight copies per k tile
+  constexpr int WCW = (WCOPIES + 7) / 8;          // per wave (the last round partial)
+  constexpr int XR = BM / 128;                    // activation rows per thread
+  static_assert(XR * 128 == BM && WCOPIES * 1024 == BN * kRowBytes, "tile shape");
+  __shared__ __attribute__((aligned(1024))) char w_lds0[BN * kRowBytes];
+  __shared__ __attribute__((aligned(1024))) char w_lds1[BN * kRowBytes];
+  __shared__ __attribute__((aligned(1024))) char xh_lds0[BM * kRowBytes];
+  __shared__ __attribute__((aligned(1024))) char xh_lds1[BM * kRowBytes];
+  __shared__ __attribute__((aligned(1024))) char xl_lds0[BM * kRowBytes];
+  __shared__ __attribute__((aligned(1024))) char xl_lds1[BM * kRowBytes];
 
-  const int tiles_n = (a.N + kBN - 1) / kBN;
+  const int tiles_n = (a.N + BN - 1) / BN;
   const int tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
-  const int m0 = tm * kBM, n0 = tn * kBN;
+  const int m0 = tm * BM, n0 = tn * BN;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const int wm = wave >> 2, wn = wave & 3;  // the wave's 64 x 64 block
+  const int wm = wave / WN, wn = wave % WN;  // the wave's TM x TN block
   const int lr = lane & 31, hl = lane >> 5;
   const int nk = a.K / kBK;
 
-  // Weight copies: 16 KB per tile = 16 copies of 1 KB, two per wave. Copy j of
-  // wave w fills LDS bytes [(2w + j) * 1024, +1024); lane l's 16 bytes land at
-  // +16 l, i.e. row R = byte / 64, position p, which holds chunk p ^ swz4(R).
+  // Weight copies: copy c = wave + 8 j fills LDS bytes [c * 1024, +1024);
+  // lane l's 16 bytes land at +16 l, i.e. row R = byte / 64, position p, which
+  // holds chunk p ^ swz4(R).
   const char *wg = reinterpret_cast<const char *>(a.w);
-  long w_src[2];
+  long w_src[WCW];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int byte = (2 * wave + j) * 1024 + lane * 16;
+  for (int j = 0; j < WCW; ++j) {
+    const int c = min(wave + 8 * j, WCOPIES - 1);
+    const int byte = c * 1024 + lane * 16;
     const int row = byte / kRowBytes, p = (byte % kRowBytes) / 16;
     const int n = min(n0 + row, a.N - 1);
     w_src[j] = (long)n * a.K * 2 + 16 * (p ^ swz4(row));
   }
   auto copy_w = [&](int kt, char *dst) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      __builtin_amdgcn_global_load_lds(wg + w_src[j] + (long)kt * kBK * 2, (lds_void *)(dst + (2 * wave + j) * 1024),
-                                       16, 0, 0);
+    for (int j = 0; j < WCW; ++j)
+      if (wave + 8 * j < WCOPIES) copy16_to_lds(wg + w_src[j] + (long)kt * kBK * 2, dst + (wave + 8 * j) * 1024);
   };
-  // Activations: thread t loads row t / 4, columns 8 (t % 4) + [0, 8) of the
-  // k tile, splits them and writes 16 bytes of hi and of lo (chunk t % 4 of
-  // the row).
+  // Activations: thread t loads rows t / 4 + 128 i, columns 8 (t % 4) + [0, 8)
+  // of the k tile, splits them and writes 16 bytes of hi and of lo (chunk
+  // t % 4 of the row).
   const int xr = tid >> 2, xc = tid & 3;
-  const float *xg = a.x + (long)min(m0 + xr, a.M - 1) * a.K + 8 * xc;
-  auto load_x = [&](int kt, float4 (&xv)[2]) {
+  const float *xg[XR];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) xv[i] = *reinterpret_cast<const float4 *>(xg + (long)kt * kBK + 4 * i);
+  for (int i = 0; i < XR; ++i) xg[i] = a.x + (long)min(m0 + xr + 128 * i, a.M - 1) * a.K + 8 * xc;
+  auto load_x = [&](int kt, float4 (&xv)[XR][2]) {
+#pragma unroll
+    for (int i = 0; i < XR; ++i)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) xv[i][e] = *reinterpret_cast<const float4 *>(xg[i] + (long)kt * kBK + 4 * e);
   };
-  auto store_x = [&](const float4 (&xv)[2], char *hi, char *lo) {
-    const float f[8] = {xv[0].x, xv[0].y, xv[0].z, xv[0].w, xv[1].x, xv[1].y, xv[1].z, xv[1].w};
-    unsigned h[4], l[4];
+  auto store_x = [&](const float4 (&xv)[XR][2], char *hi, char *lo) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      // one v_cvt_pk_bf16_f32 per pair (round to nearest even), for hi and for lo
-      h[i] = bf16x2_rne(f[2 * i], f[2 * i + 1]);
-      const float r0 = f[2 * i] - __uint_as_float(h[i] << 16);
-      const float r1 = f[2 * i + 1] - __uint_as_float(h[i] & 0xffff0000u);
-      l[i] = bf16x2_rne(r0, r1);
+    for (int r = 0; r < XR; ++r) {
+      const float f[8] = {xv[r][0].x, xv[r][0].y, xv[r][0].z, xv[r][0].w, xv[r][1].x, xv[r][1].y, xv[r][1].z, xv[r][1].w};
+      unsigned h[4], l[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        // one v_cvt_pk_bf16_f32 per pair (round to nearest even), for hi and for lo
+        h[i] = bf16x2_rne(f[2 * i], f[2 * i + 1]);
+        const float r0 = f[2 * i] - __uint_as_float(h[i] << 16);
+        const float r1 = f[2 * i + 1] - __uint_as_float(h[i] & 0xffff0000u);
+        l[i] = bf16x2_rne(r0, r1);
+      }
+      const int row = xr + 128 * r;
+      const int off = row * kRowBytes + 16 * (xc ^ swz4(row));
+      *reinterpret_cast<uint4 *>(hi + off) = make_uint4(h[0], h[1], h[2], h[3]);
+      *reinterpret_cast<uint4 *>(lo + off) = make_uint4(l[0], l[1], l[2], l[3]);
     }
-    const int off = xr * kRowBytes + 16 * (xc ^ swz4(xr));
-    *reinterpret_cast<uint4 *>(hi + off) = make_uint4(h[0], h[1], h[2], h[3]);
-    *reinterpret_cast<uint4 *>(lo + off) = make_uint4(l[0], l[1], l[2], l[3]);
   };
 
-  // Fragment offsets: block b of the wave's 64 x 64 block, 16-deep k step s: row
-  // 32 b + lr, chunk 2 s + hl (32 b leaves swz4 unchanged).
-  unsigned a_rd[2][2], b_rd[2][2];
+  // Fragment offsets: block b of the wave's block, 16-deep k step s: row
+  // 32 b + lr of it, chunk 2 s + hl (TM, TN and 32 b are multiples of 32 and
+  // leave swz4 unchanged).
+  unsigned a_rd[BI][2], b_rd[BJ][2];
 #pragma unroll
-  for (int b = 0; b < 2; ++b)
+  for (int s = 0; s < 2; ++s) {
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int ra = wm * 64 + 32 * b + lr, rb = wn * 64 + 32 * b + lr;
+    for (int b = 0; b < BI; ++b) {
+      const int ra = wm * TM + 32 * b + lr;
       a_rd[b][s] = ra * kRowBytes + 16 * ((2 * s + hl) ^ swz4(ra));
+    }
+#pragma unroll
+    for (int b = 0; b < BJ; ++b) {
+      const int rb = wn * TN + 32 * b + lr;
       b_rd[b][s] = rb * kRowBytes + 16 * ((2 * s + hl) ^ swz4(rb));
     }
+  }
 
-  f32x16 acc[2][2];
+  f32x16 acc[BI][BJ];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < BI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < BJ; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
   auto compute = [&](const char *wl, const char *xh, const char *xl) {
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      bf16x8 fa_h[2], fa_l[2], fb[2];
+      bf16x8 fa_h[BI], fa_l[BI], fb[BJ];
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
+      for (int b = 0; b < BI; ++b) {
         fa_h[b] = *reinterpret_cast<const bf16x8 *>(xh + a_rd[b][s]);
         fa_l[b] = *reinterpret_cast<const bf16x8 *>(xl + a_rd[b][s]);
-        fb[b] = *reinterpret_cast<const bf16x8 *>(wl + b_rd[b][s]);
       }
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int b = 0; b < BJ; ++b) fb[b] = *reinterpret_cast<const bf16x8 *>(wl + b_rd[b][s]);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa_h[i], fb[j], acc[i][j], 0, 0, 0);
+      for (int i = 0; i < BI; ++i)
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+        for (int j = 0; j < BJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa_h[i], fb[j], acc[i][j], 0, 0, 0);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa_l[i], fb[j], acc[i][j], 0, 0, 0);
+      for (int i = 0; i < BI; ++i)
+#pragma unroll
+        for (int j = 0; j < BJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa_l[i], fb[j], acc[i][j], 0, 0, 0);
     }
   };
 
   // One step on tile t; B selects the buffers (t % 2 computes, (t+1) % 2
   // receives): the weights of tile t+1 are copied one step ahead, the
   // activations loaded two ahead and written one ahead.
-  auto step = [&](auto B_, int t, float4 (&xnext)[2]) {
+  auto step = [&](auto B_, int t, float4 (&xnext)[XR][2]) {
     constexpr int B = decltype(B_)::value;
     char *const w_cur = B ? w_lds1 : w_lds0, *const w_fill = B ? w_lds0 : w_lds1;
     char *const xh_cur = B ? xh_lds1 : xh_lds0, *const xl_cur = B ? xl_lds1 : xl_lds0;
@@ -356,19 +401,19 @@ __global__ __launch_bounds__(512, 2) void linear_gemm_kernel(const LinearArgs a)
     if (more) load_x(t + 2, xnext);
     compute(w_cur, xh_cur, xl_cur);
     // everything but this step's activation loads is done
-    if (more) __builtin_amdgcn_s_waitcnt(0x0F72);  // vmcnt(2)
-    else __builtin_amdgcn_s_waitcnt(0x0F70);       // vmcnt(0)
+    if (more) wait_vmcnt<2 * XR>();
+    else wait_vmcnt<0>();
     __syncthreads();
   };
 
   // Prologue: weights of tile 0 copied, activations of tile 0 in LDS, tile
   // 1's in registers.
-  float4 xv[2];
+  float4 xv[XR][2];
   copy_w(0, w_lds0);
   load_x(0, xv);
   store_x(xv, xh_lds0, xl_lds0);
   if (nk > 1) load_x(1, xv);
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  wait_vmcnt<0>();
   __syncthreads();
 
   using I0 = std::integral_constant<int, 0>;
@@ -383,15 +428,15 @@ __global__ __launch_bounds__(512, 2) void linear_gemm_kernel(const LinearArgs a)
   // Accumulator layout: element e of lane l is row 8 (e / 4) + 4 hl + e % 4,
   // column lr of its 32 x 32 block.
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int n = n0 + wn * 64 + 32 * j + lr;
+  for (int j = 0; j < BJ; ++j) {
+    const int n = n0 + wn * TN + 32 * j + lr;
     if (n >= a.N) continue;
     const float bn = a.bias ? a.bias[n] : 0.0f;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < BI; ++i)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int m = m0 + wm * 64 + 32 * i + 8 * (e >> 2) + 4 * hl + (e & 3);
+        const int m = m0 + wm * TM + 32 * i + 8 * (e >> 2) + 4 * hl + (e & 3);
         if (m < a.M) a.out[(long)m * a.N + n] = bn + acc[i][j][e];
       }
   }
@@ -527,6 +572,12 @@ hipError_t launch_generic_linear(hipStream_t st, const LinearArgs &a) {
   hipLaunchKernelGGL((linear_generic_kernel<WT>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a);
   return hipGetLastError();
 }
+template <int BM, int BN, int WM, int WN, int MINWG>
+hipError_t launch_gemm(hipStream_t st, const LinearArgs &a) {
+  const long grid = (long)((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+  hipLaunchKernelGGL((linear_gemm_kernel<BM, BN, WM, WN, MINWG>), dim3((unsigned)grid), dim3(512), 0, st, a);
+  return hipGetLastError();
+}
 template <typename WT>
 hipError_t launch_typed(hipStream_t st, const LinearArgs &a, int path) {
   if (path == kLinearGemv) return launch_gemv<WT>(st, a);
@@ -568,6 +619,18 @@ hipError_t launch_linear_multi(hipStream_t st, const LinearArgs *segs, int n) {
   }
 }
 
+// The 256 x 320 tiles when their rounds of one workgroup per CU, each tile
+// 2.5 times the work of a 128 x 256 one at the same rate per CU, take less
+// time than the 128 x 256 tiles' rounds of two per CU (4096 x 5120: 640
+// tiles of 128 x 256, a second round a quarter full, against 256 wide tiles
+// in one round).
+static bool linear_gemm_wide(long M, long N, int cus) {
+  const long c = cus > 0 ? cus : 256;
+  const long small = ((M + 127) / 128) * ((N + 255) / 256), wide = ((M + 255) / 256) * ((N + 319) / 320);
+  const long rounds_small = (small + 2 * c - 1) / (2 * c), rounds_wide = (wide + c - 1) / c;
+  return 5 * rounds_wide < 4 * rounds_small;
+}
+
 hipError_t launch_linear(hipStream_t st, const LinearArgs &a, int path) {
   if (a.M <= 0 || a.N <= 0) return hipSuccess;
   if (a.norm_w && path != kLinearGemv) return hipErrorInvalidValue;  // the folded norm is the GEMV's
@@ -584,9 +647,8 @@ hipError_t launch_linear(hipStream_t st, const LinearArgs &a, int path) {
   }
   if (path == kLinearGemm) {
     if (a.dtype != SPISSA_DTYPE_BF16 || a.K % kBK != 0) return hipErrorInvalidValue;
-    const long grid = (long)((a.M + kBM - 1) / kBM) * ((a.N + kBN - 1) / kBN);
-    hipLaunchKernelGGL(linear_gemm_kernel, dim3((unsigned)grid), dim3(512), 0, st, a);
-    return hipGetLastError();
+    return linear_gemm_wide(a.M, a.N, a.cus) ? launch_gemm<256, 320, 4, 2, 1>(st, a)
+                                              : launch_gemm<128, 256, 2, 4, 2>(st, a);
   }
   switch (a.dtype) {
     case SPISSA_DTYPE_F32: return launch_typed<float>(st, a, path);

@@ -116,6 +116,22 @@ def test_llama3b_fused_qkv_prefill_4096(gpu):
     assert np.isfinite(got).all()
 
 
+def test_wide_tile_gemm_ragged_edges(gpu):
+    # 4000 x 5100 outputs take the 256 x 320 tiles (one round of 256; 128 x 256
+    # tiles would need 640 workgroups): the last row and column tiles are
+    # partial, and K = 96 is an odd number of 32-deep k tiles.
+    batch, in_f, out_f = 4000, 96, 5100
+    w = weight(out_f, in_f, DTYPE_BF16, "wide")
+    x = acts(batch, in_f, "wide")
+    bias = normal_f32(seed(5, out_f, in_f, "b"), out_f)
+    got = sa.linear(sa.LinearWeight(w, DTYPE_BF16, out_f, in_f), x, bias,
+                    StreamingLinearConfig(batch, in_f, out_f))
+    pick = np.array([0, 1, 255, 256, 1777, 3839, 3840, 3998, 3999])
+    ref = o.linear(x.reshape(batch, in_f)[pick].ravel().copy(), w, o.DTYPE_BF16, bias, len(pick), in_f, out_f)
+    check_close(got.reshape(batch, out_f)[pick].ravel(), ref, "wide tiles 4000 x 5100 x 96")
+    assert np.isfinite(got).all()
+
+
 @pytest.mark.parametrize("dtype", [DTYPE_F16, DTYPE_F32])
 @pytest.mark.parametrize("batch", [1, 3])
 def test_f16_f32_weights_gemv(gpu, dtype, batch):
