@@ -164,7 +164,7 @@ __global__ __launch_bounds__(256, 4) void decode_split_kernel(const DecodeArgs a
   __shared__ float red_o[NG][RB][D];
   __shared__ float red_l[NG][RB];
   __shared__ float wave_m[4][RB];
-  __shared__ float knorm_sq[D];  // squares of the new key (fused QK-norm)
+  __shared__ __attribute__((aligned(16))) float knorm_sq[D];  // squares of the new key (fused QK-norm)
 
   // Head blocks are the fastest grid dimension: the workgroups that read the
   // same key rows (all KV heads of one split) are dispatched back to back.
@@ -321,8 +321,29 @@ __global__ __launch_bounds__(256, 4) void decode_split_kernel(const DecodeArgs a
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       float inv = 0.0f;
       if (lane == 0) {
+        // The chain reads 16 squares ahead of the ones it adds, so the LDS
+        // latency overlaps the adds (the same order of additions).
+        const float4 *sq4 = reinterpret_cast<const float4 *>(knorm_sq);
+        float4 cur[4], nxt[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) cur[j] = sq4[j];
         float acc = 0.0f;
-        for (int c = 0; c < D; ++c) acc += knorm_sq[c];
+#pragma unroll
+        for (int it = 0; it < D / 16; ++it) {
+          if (it + 1 < D / 16) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) nxt[j] = sq4[4 * (it + 1) + j];
+          }
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            acc += cur[j].x;
+            acc += cur[j].y;
+            acc += cur[j].z;
+            acc += cur[j].w;
+          }
+#pragma unroll
+          for (int j = 0; j < 4; ++j) cur[j] = nxt[j];
+        }
         inv = 1.0f / sqrtf(acc / (float)D + a.norm_eps);
       }
       inv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv), 0));
