@@ -387,31 +387,49 @@ __global__ __launch_bounds__(RPW * 4) void prefill_append_kernel(
     *reinterpret_cast<float4 *>(o + 4) = *reinterpret_cast<const float4 *>(p + off(z, 1));
   };
   // QK-norm (with NORM) and rotate_neox_pair (rotary.rs:467-481) at `pos`.
+  // The 16-row form (short chunks: latency-bound, few waves) loads every
+  // chunk's weights and table rows before the sum of squares, so their
+  // latency runs beside it (Gemma-3-4B chunk of 128 on 16384: 1.044 -> 0.992
+  // ms over 34 layers); the 64-row form loads them chunk by chunk after it,
+  // keeping the registers for residency (the same early loads took Gemma-3-1B's
+  // 4096-token prefill from 1.10-1.12 to 1.14 ms).
+  constexpr bool EARLY = RPW < 64;
   auto norm_rotate = [&](const float *w, long pos) {
+    float wl[EARLY ? G : 1][8], wh[EARLY ? G : 1][8], cs[EARLY ? G : 1][8], sn[EARLY ? G : 1][8];
+    auto load_chunk = [&](int z, int i) {
+      if constexpr (NORM) {
+        load8(w, z, wl[i]);
+        load8(w + HALF, z, wh[i]);
+      }
+      if (cos_tab) {
+        load8(cos_tab + pos * HALF, z, cs[i]);
+        load8(sin_tab + pos * HALF, z, sn[i]);
+      }
+    };
+    if constexpr (EARLY) {
+#pragma unroll
+      for (int z = 0; z < G; ++z) load_chunk(z, z);
+    }
     float inv = 1.0f;
     if constexpr (NORM) inv = quad_inv_rms<D>(x, c, nrm.eps);
 #pragma unroll
     for (int z = 0; z < G; ++z) {
+      const int i = EARLY ? z : 0;
+      if constexpr (!EARLY) load_chunk(z, 0);
       float *a = reinterpret_cast<float *>(x[0][z]), *b = reinterpret_cast<float *>(x[1][z]);
       if constexpr (NORM) {
-        float wl[8], wh[8];
-        load8(w, z, wl);
-        load8(w + HALF, z, wh);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          a[j] = a[j] * inv * wl[j];
-          b[j] = b[j] * inv * wh[j];
+          a[j] = a[j] * inv * wl[i][j];
+          b[j] = b[j] * inv * wh[i][j];
         }
       }
       if (cos_tab) {
-        float cs[8], sn[8];
-        load8(cos_tab + pos * HALF, z, cs);
-        load8(sin_tab + pos * HALF, z, sn);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const float first = a[j], second = b[j];
-          a[j] = first * cs[j] - second * sn[j];
-          b[j] = second * cs[j] + first * sn[j];
+          a[j] = first * cs[i][j] - second * sn[i][j];
+          b[j] = second * cs[i][j] + first * sn[i][j];
         }
       }
     }
