@@ -321,28 +321,30 @@ __global__ __launch_bounds__(256, 4) void decode_split_kernel(const DecodeArgs a
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       float inv = 0.0f;
       if (lane == 0) {
-        // The chain reads 16 squares ahead of the ones it adds, so the LDS
-        // latency overlaps the adds (the same order of additions).
+        // The chain reads D/16 squares ahead of the ones it adds, so the LDS
+        // latency overlaps the adds (the same order of additions; the read
+        // ahead scales with D so that head_dim 64 stays within 128 VGPRs).
+        constexpr int CH = D / 64, NIT = D / (4 * CH);
         const float4 *sq4 = reinterpret_cast<const float4 *>(knorm_sq);
-        float4 cur[4], nxt[4];
+        float4 cur[CH], nxt[CH];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) cur[j] = sq4[j];
+        for (int j = 0; j < CH; ++j) cur[j] = sq4[j];
         float acc = 0.0f;
 #pragma unroll
-        for (int it = 0; it < D / 16; ++it) {
-          if (it + 1 < D / 16) {
+        for (int it = 0; it < NIT; ++it) {
+          if (it + 1 < NIT) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) nxt[j] = sq4[4 * (it + 1) + j];
+            for (int j = 0; j < CH; ++j) nxt[j] = sq4[CH * (it + 1) + j];
           }
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
+          for (int j = 0; j < CH; ++j) {
             acc += cur[j].x;
             acc += cur[j].y;
             acc += cur[j].z;
             acc += cur[j].w;
           }
 #pragma unroll
-          for (int j = 0; j < 4; ++j) cur[j] = nxt[j];
+          for (int j = 0; j < CH; ++j) cur[j] = nxt[j];
         }
         inv = 1.0f / sqrtf(acc / (float)D + a.norm_eps);
       }
